@@ -1,0 +1,450 @@
+// The C ABI of include/bchip.h: context, device memory, argument checks and dispatch.
+//
+// It stands where bc-infer's CUDA backend stands (crates/bc-infer/src/gpu/cuda.rs:1-95):
+// one device, one stream, launches queued back to back and waited for by bchip_sync. Each
+// entry point checks its arguments on the host before anything reaches the GPU: shapes the
+// kernels assume, alignment, and, for buffers this library allocated, that every byte a
+// kernel will touch lies inside them. Errors come back as codes with a thread-local
+// message; nothing aborts across the ABI.
+#include "bchip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+using namespace bchip;
+
+struct bchip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    Workspace ws;
+    std::map<uintptr_t, size_t> allocs;  // base -> bytes, of bchip_alloc memory
+    std::string name;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorOutOfMemory) return fail(BCHIP_E_OOM, "%s: %s", what, hipGetErrorString(e));
+    return fail(BCHIP_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                       \
+    do {                                          \
+        hipError_t e_ = (expr);                   \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+int enter(bchip_ctx* c) {
+    if (!c) return fail(BCHIP_E_ARG, "no context");
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return BCHIP_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// For memory this library allocated, that [p, p + bytes) lies inside one allocation.
+// Memory from elsewhere cannot be checked and is trusted.
+int check_span(const bchip_ctx* c, const void* p, uint64_t bytes, const char* what) {
+    if (c->allocs.empty() || bytes == 0) return BCHIP_OK;
+    const uintptr_t a = (uintptr_t)p;
+    auto it = c->allocs.upper_bound(a);
+    if (it == c->allocs.begin()) return BCHIP_OK;
+    --it;
+    if (a >= it->first + it->second) return BCHIP_OK;  // not ours
+    if (a + bytes > it->first + it->second)
+        return fail(BCHIP_E_ARG, "%s: %llu bytes from offset %llu pass the end of its %llu-byte buffer", what,
+                    (unsigned long long)bytes, (unsigned long long)(a - it->first), (unsigned long long)it->second);
+    return BCHIP_OK;
+}
+
+uint32_t esize(uint32_t type) { return type == BCHIP_F16 ? 2u : 4u; }
+
+// Bytes from p to the end of the bchip_alloc allocation holding it, or UINT64_MAX for
+// memory this library did not allocate.
+uint64_t bytes_left(const bchip_ctx* c, const void* p) {
+    const uintptr_t a = (uintptr_t)p;
+    auto it = c->allocs.upper_bound(a);
+    if (it == c->allocs.begin()) return UINT64_MAX;
+    --it;
+    if (a >= it->first + it->second) return UINT64_MAX;
+    return it->first + it->second - a;
+}
+
+#define CHECK(expr)                  \
+    do {                             \
+        int rc_ = (expr);            \
+        if (rc_ != BCHIP_OK) return rc_; \
+    } while (0)
+
+int check_heads(uint32_t nh, uint32_t nkv, uint32_t hd) {
+    if (nh == 0 || nkv == 0 || nh % nkv != 0)
+        return fail(BCHIP_E_UNSUPPORTED, "%u query heads do not share %u KV heads evenly", nh, nkv);
+    if (nh / nkv > 16) return fail(BCHIP_E_UNSUPPORTED, "group of %u query heads per KV head (at most 16)", nh / nkv);
+    if (hd == 0 || hd % 8 != 0 || hd > MAX_HD)
+        return fail(BCHIP_E_UNSUPPORTED, "head_dim %u (a multiple of 8 up to %u)", hd, MAX_HD);
+    return BCHIP_OK;
+}
+
+}  // namespace
+
+namespace bchip {
+
+hipError_t Workspace::reserve(size_t need_slots, size_t hd_pad) {
+    if (need_slots <= slots && hd_pad <= hdp && o) return hipSuccess;
+    size_t ns = std::max(need_slots, slots), nh = std::max(hd_pad, hdp);
+    release();
+    hipError_t e = hipMalloc((void**)&o, ns * nh * sizeof(float));
+    if (e != hipSuccess) return e;
+    e = hipMalloc((void**)&ml, ns * 2 * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipFree(o);
+        o = nullptr;
+        return e;
+    }
+    slots = ns;
+    hdp = nh;
+    return hipSuccess;
+}
+
+void Workspace::release() {
+    if (o) (void)hipFree(o);
+    if (ml) (void)hipFree(ml);
+    o = ml = nullptr;
+    slots = hdp = 0;
+}
+
+}  // namespace bchip
+
+extern "C" {
+
+const char* bchip_last_error(void) { return g_err.c_str(); }
+
+int bchip_abi_version(void) { return BCHIP_ABI_VERSION; }
+
+int bchip_init(int device, bchip_ctx** out) {
+    if (!out) return fail(BCHIP_E_ARG, "no output pointer");
+    *out = nullptr;
+    const char* env = getenv("BC_INFER_GPU");
+    if (env && strcmp(env, "0") == 0) return fail(BCHIP_E_DISABLED, "BC_INFER_GPU=0 turns the GPU off");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(BCHIP_E_NODEV, "no HIP device");
+    if (device < 0 || device >= n) return fail(BCHIP_E_NODEV, "device %d of %d", device, n);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(BCHIP_E_NODEV, "device %d is %s; these kernels are built for gfx950", device, prop.gcnArchName);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    bchip_ctx* c = new bchip_ctx();
+    c->device = device;
+    c->name = prop.name;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&c->t0);
+    if (e == hipSuccess) e = hipEventCreate(&c->t1);
+    if (e != hipSuccess) {
+        bchip_destroy(c);
+        return hip_fail(e, "creating the stream");
+    }
+    *out = c;
+    return BCHIP_OK;
+}
+
+int bchip_destroy(bchip_ctx* c) {
+    if (!c) return BCHIP_OK;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    c->ws.release();
+    for (auto& a : c->allocs) (void)hipFree((void*)a.first);
+    if (c->t0) (void)hipEventDestroy(c->t0);
+    if (c->t1) (void)hipEventDestroy(c->t1);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return BCHIP_OK;
+}
+
+int bchip_device_name(bchip_ctx* c, char* buf, size_t len) {
+    CHECK(enter(c));
+    if (!buf || len == 0) return fail(BCHIP_E_ARG, "no buffer");
+    snprintf(buf, len, "%s", c->name.c_str());
+    return BCHIP_OK;
+}
+
+int bchip_mem_free(bchip_ctx* c, uint64_t* free_bytes) {
+    CHECK(enter(c));
+    if (!free_bytes) return fail(BCHIP_E_ARG, "no output pointer");
+    size_t f = 0, t = 0;
+    HIP_TRY(hipMemGetInfo(&f, &t), "hipMemGetInfo");
+    *free_bytes = f;
+    return BCHIP_OK;
+}
+
+int bchip_unified(bchip_ctx* c, int* unified) {
+    CHECK(enter(c));
+    if (!unified) return fail(BCHIP_E_ARG, "no output pointer");
+    *unified = 0;
+    return BCHIP_OK;
+}
+
+int bchip_alloc(bchip_ctx* c, size_t bytes, void** dev) {
+    CHECK(enter(c));
+    if (!dev) return fail(BCHIP_E_ARG, "no output pointer");
+    *dev = nullptr;
+    if (bytes == 0) bytes = 1;
+    void* p = nullptr;
+    HIP_TRY(hipMalloc(&p, bytes), "hipMalloc");
+    hipError_t e = hipMemsetAsync(p, 0, bytes, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return hip_fail(e, "zeroing a new buffer");
+    }
+    c->allocs[(uintptr_t)p] = bytes;
+    *dev = p;
+    return BCHIP_OK;
+}
+
+int bchip_free(bchip_ctx* c, void* dev) {
+    CHECK(enter(c));
+    if (!dev) return BCHIP_OK;
+    auto it = c->allocs.find((uintptr_t)dev);
+    if (it == c->allocs.end()) return fail(BCHIP_E_ARG, "%p was not allocated by this context", dev);
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    HIP_TRY(hipFree(dev), "hipFree");
+    c->allocs.erase(it);
+    return BCHIP_OK;
+}
+
+int bchip_upload(bchip_ctx* c, void* dev, size_t off, const void* host, size_t bytes) {
+    CHECK(enter(c));
+    if (bytes == 0) return BCHIP_OK;
+    if (!dev || !host) return fail(BCHIP_E_ARG, "null pointer");
+    CHECK(check_span(c, (char*)dev + off, bytes, "upload"));
+    HIP_TRY(hipMemcpyAsync((char*)dev + off, host, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return BCHIP_OK;
+}
+
+int bchip_download(bchip_ctx* c, const void* dev, size_t off, void* host, size_t bytes) {
+    CHECK(enter(c));
+    if (bytes == 0) return BCHIP_OK;
+    if (!dev || !host) return fail(BCHIP_E_ARG, "null pointer");
+    CHECK(check_span(c, (const char*)dev + off, bytes, "download"));
+    HIP_TRY(hipMemcpyAsync(host, (const char*)dev + off, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return BCHIP_OK;
+}
+
+int bchip_sync(bchip_ctx* c) {
+    CHECK(enter(c));
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return BCHIP_OK;
+}
+
+int bchip_stream(bchip_ctx* c, void** s) {
+    CHECK(enter(c));
+    if (!s) return fail(BCHIP_E_ARG, "no output pointer");
+    *s = (void*)c->stream;
+    return BCHIP_OK;
+}
+
+int bchip_rope(bchip_ctx* c, float* x, const float* inv_freq, const uint32_t* positions, uint32_t rows,
+               uint32_t heads, uint32_t hd, uint32_t rope_dim, uint32_t neox) {
+    CHECK(enter(c));
+    if (rows == 0 || heads == 0) return BCHIP_OK;
+    if (!x || !inv_freq || !positions) return fail(BCHIP_E_ARG, "null pointer");
+    if (rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
+    CHECK(check_span(c, x, (uint64_t)rows * heads * hd * 4, "x"));
+    CHECK(check_span(c, positions, (uint64_t)rows * 4, "positions"));
+    CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
+    HIP_TRY(rope_launch(x, inv_freq, positions, rows, heads, hd, rope_dim, neox, c->stream), "rope");
+    return BCHIP_OK;
+}
+
+int bchip_copy(bchip_ctx* c, const void* src, uint32_t st, void* dst, uint32_t dt, uint64_t off, uint64_t n) {
+    CHECK(enter(c));
+    if (n == 0) return BCHIP_OK;
+    if (!src || !dst) return fail(BCHIP_E_ARG, "null pointer");
+    if (st > 1 || dt > 1) return fail(BCHIP_E_ARG, "element types %u, %u", st, dt);
+    CHECK(check_span(c, src, n * esize(st), "copy source"));
+    CHECK(check_span(c, (const char*)dst + off * esize(dt), n * esize(dt), "copy destination"));
+    HIP_TRY(copy_launch(src, st, dst, dt, off, n, c->stream), "copy");
+    return BCHIP_OK;
+}
+
+int bchip_move(bchip_ctx* c, void* buf, uint32_t type, uint64_t from, uint64_t to, uint64_t n) {
+    CHECK(enter(c));
+    if (n == 0) return BCHIP_OK;
+    if (!buf) return fail(BCHIP_E_ARG, "null pointer");
+    if (type > 1) return fail(BCHIP_E_ARG, "element type %u", type);
+    if (to > from) return fail(BCHIP_E_ARG, "move to %llu after from %llu", (unsigned long long)to,
+                                (unsigned long long)from);
+    CHECK(check_span(c, buf, (from + n) * esize(type), "move"));
+    HIP_TRY(move_launch(buf, type, from, to, n, c->stream), "move");
+    return BCHIP_OK;
+}
+
+int bchip_keep(bchip_ctx* c, void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width, uint64_t base,
+               const uint32_t* rows, uint32_t nrows) {
+    CHECK(enter(c));
+    if (nbufs == 0 || nrows == 0) return BCHIP_OK;
+    if (!bufs || !rows) return fail(BCHIP_E_ARG, "null pointer");
+    if (type > 1) return fail(BCHIP_E_ARG, "element type %u", type);
+    if (nrows > 64) return fail(BCHIP_E_ARG, "%u rows (at most 64)", nrows);
+    for (uint32_t i = 0; i + 1 < nrows; i++)
+        if (rows[i] >= rows[i + 1]) return fail(BCHIP_E_ARG, "rows are not an ascending path");
+    const uint64_t end = (base + rows[nrows - 1] + 1) * width * esize(type);
+    for (uint32_t b = 0; b < nbufs; b++) {
+        if (!bufs[b]) return fail(BCHIP_E_ARG, "null buffer %u", b);
+        CHECK(check_span(c, bufs[b], end, "keep"));
+    }
+    HIP_TRY(keep_launch(bufs, nbufs, type, width, base, rows, nrows, c->stream), "keep");
+    return BCHIP_OK;
+}
+
+int bchip_rope_append(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc, uint32_t kv_type,
+                      const float* inv_freq, const uint32_t* positions, uint32_t rows, uint32_t nh, uint32_t nkv,
+                      uint32_t hd, uint32_t rope_dim, uint32_t neox, uint64_t slot0) {
+    CHECK(enter(c));
+    if (rows == 0) return BCHIP_OK;
+    if (!q || !k || !v || !kc || !vc || !inv_freq || !positions) return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    if (hd % 2 || rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
+    if (nh == 0 || nkv == 0) return fail(BCHIP_E_ARG, "no heads");
+    const uint64_t kvd = (uint64_t)nkv * hd;
+    CHECK(check_span(c, q, (uint64_t)rows * nh * hd * 4, "q"));
+    CHECK(check_span(c, k, rows * kvd * 4, "k"));
+    CHECK(check_span(c, v, rows * kvd * 4, "v"));
+    CHECK(check_span(c, kc, (slot0 + rows) * kvd * esize(kv_type), "kc"));
+    CHECK(check_span(c, vc, (slot0 + rows) * kvd * esize(kv_type), "vc"));
+    CHECK(check_span(c, positions, (uint64_t)rows * 4, "positions"));
+    HIP_TRY(rope_append_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, rows, nh, nkv, hd, rope_dim, neox,
+                               slot0, c->stream),
+            "rope_append");
+    return BCHIP_OK;
+}
+
+int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc, uint32_t kv_type, float* out,
+                    const uint32_t* masks, uint32_t tree, uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd,
+                    uint32_t pos, float scale) {
+    CHECK(enter(c));
+    if (rows == 0) return BCHIP_OK;
+    if (!q || !kc || !vc || !out) return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    CHECK(check_heads(nh, nkv, hd));
+    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc))
+        return fail(BCHIP_E_ARG, "q, out and the caches must be 16-byte aligned");
+    if ((uint64_t)pos + rows > 0xffffffffull) return fail(BCHIP_E_ARG, "position past 2^32");
+    if (tree) {
+        if (!masks) return fail(BCHIP_E_ARG, "a tree needs its masks");
+        if (rows > MAX_ITEMS) return fail(BCHIP_E_ARG, "a tree pass of %u rows (at most %u)", rows, MAX_ITEMS);
+        CHECK(check_span(c, masks, (uint64_t)rows * 8, "masks"));
+    }
+    const uint64_t kvd = (uint64_t)nkv * hd, slots = (uint64_t)pos + rows;
+    CHECK(check_span(c, q, (uint64_t)rows * nh * hd * 4, "q"));
+    CHECK(check_span(c, out, (uint64_t)rows * nh * hd * 4, "out"));
+    CHECK(check_span(c, kc, slots * kvd * esize(kv_type), "kc"));
+    CHECK(check_span(c, vc, slots * kvd * esize(kv_type), "vc"));
+    const uint64_t row_bytes = kvd * esize(kv_type);
+    const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / row_bytes;
+    AttnCall a{q, kc, vc, kv_type, out, masks, tree ? 1u : 0u, rows, nh, nkv, hd, pos, scale, limit};
+    hipError_t e;
+    if (rows == 1 || tree) {
+        const uint32_t chunk = rows == 1 ? decode_chunk(slots) : CHUNK_MULTI;
+        Item items[MAX_ITEMS];
+        for (uint32_t r = 0; r < rows; r++) {
+            const uint64_t upto = tree ? slots : (uint64_t)pos + r + 1;
+            items[r] = Item{r, (uint32_t)upto, 0u, (uint32_t)((upto + chunk - 1) / chunk), chunk, 0ull};
+        }
+        e = direct_attention(a, items, rows, c->ws, c->stream);
+    } else {
+        e = shared_attention(a, c->ws, c->stream);
+    }
+    HIP_TRY(e, "attention");
+    return BCHIP_OK;
+}
+
+int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const void* vc, uint32_t kv_type,
+                           float* out, const uint32_t* seq_lens, const uint64_t* kv_offsets, uint32_t nseq,
+                           uint32_t nh, uint32_t nkv, uint32_t hd, float scale) {
+    CHECK(enter(c));
+    if (nseq == 0) return BCHIP_OK;
+    if (!q || !kc || !vc || !out || !seq_lens || !kv_offsets) return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    if (nseq > 256) return fail(BCHIP_E_ARG, "%u sequences (at most 256)", nseq);
+    CHECK(check_heads(nh, nkv, hd));
+    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc))
+        return fail(BCHIP_E_ARG, "q, out and the caches must be 16-byte aligned");
+    const uint64_t kvd = (uint64_t)nkv * hd;
+    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
+    CHECK(check_span(c, out, (uint64_t)nseq * nh * hd * 4, "out"));
+    for (uint32_t i = 0; i < nseq; i++) {
+        if (seq_lens[i] == 0) return fail(BCHIP_E_ARG, "sequence %u sees no slots", i);
+        const uint64_t end = (kv_offsets[i] + seq_lens[i]) * kvd * esize(kv_type);
+        CHECK(check_span(c, kc, end, "kc"));
+        CHECK(check_span(c, vc, end, "vc"));
+    }
+    const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
+    AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, 0u, scale, limit};
+    for (uint32_t s0 = 0; s0 < nseq; s0 += MAX_ITEMS) {
+        const uint32_t ns = std::min<uint32_t>(MAX_ITEMS, nseq - s0);
+        Item items[MAX_ITEMS];
+        for (uint32_t i = 0; i < ns; i++) {
+            const uint32_t len = seq_lens[s0 + i];
+            const uint32_t chunk = decode_chunk(len);
+            items[i] = Item{s0 + i, len, 0u, (len + chunk - 1) / chunk, chunk, kv_offsets[s0 + i]};
+        }
+        HIP_TRY(direct_attention(a, items, ns, c->ws, c->stream), "ragged attention");
+    }
+    return BCHIP_OK;
+}
+
+int bchip_fill_normal(bchip_ctx* c, void* dst, uint32_t type, uint64_t n, uint64_t seed) {
+    CHECK(enter(c));
+    if (n == 0) return BCHIP_OK;
+    if (!dst) return fail(BCHIP_E_ARG, "null pointer");
+    if (type > 1) return fail(BCHIP_E_ARG, "element type %u", type);
+    CHECK(check_span(c, dst, n * esize(type), "fill"));
+    HIP_TRY(fill_normal_launch(dst, type, n, seed, c->stream), "fill_normal");
+    return BCHIP_OK;
+}
+
+int bchip_timer_start(bchip_ctx* c) {
+    CHECK(enter(c));
+    HIP_TRY(hipEventRecord(c->t0, c->stream), "hipEventRecord");
+    return BCHIP_OK;
+}
+
+int bchip_timer_stop(bchip_ctx* c, float* ms) {
+    CHECK(enter(c));
+    if (!ms) return fail(BCHIP_E_ARG, "no output pointer");
+    HIP_TRY(hipEventRecord(c->t1, c->stream), "hipEventRecord");
+    HIP_TRY(hipEventSynchronize(c->t1), "hipEventSynchronize");
+    HIP_TRY(hipEventElapsedTime(ms, c->t0, c->t1), "hipEventElapsedTime");
+    return BCHIP_OK;
+}
+
+}  // extern "C"

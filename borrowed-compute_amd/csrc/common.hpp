@@ -1,0 +1,95 @@
+// Shared definitions of the bchip HIP sources: element types, the CDNA4 MFMA tile used by
+// every attention kernel, and the launch plans the C ABI hands to the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bchip {
+
+typedef _Float16 f16;
+typedef f16 half8 __attribute__((ext_vector_type(8)));
+typedef f16 half4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// List entries (visible KV slots) per attention block: four 16-key MFMA tiles.
+constexpr int BLK = 64;
+// List entries per chunk in every multi-row call. A row's result is the left fold of its
+// chunks' (max, sum, weighted values), each chunk an online softmax over its blocks from
+// a fresh state, so a chunk may be computed by any workgroup and the row's bits do not
+// change: that is what lets a speculative verify split across CUs and still match a
+// prefill row exactly.
+constexpr uint32_t CHUNK_MULTI = 256;
+// Largest head dimension (the reference's MAX_HEAD, kernels.h:31).
+constexpr uint32_t MAX_HD = 256;
+// Rows a tree pass may hold (model.rs:408), and items one direct launch takes.
+constexpr uint32_t MAX_ITEMS = 64;
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+// One 16x16x32 f16 MFMA with f32 accumulate (gfx950). Lane l holds A[l%16][8(l/16)+j],
+// B[8(l/16)+j][l%16] (j < 8) and D[4(l/16)+i][l%16] (i < 4).
+__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// A row of work for the direct (one wave, one 16-slot tile) attention kernel: the G query
+// heads of one row against one KV head.
+struct Item {
+    uint32_t row;    // row of q / out
+    uint32_t len;    // visible list length (tree rows: computed from the mask)
+    uint32_t unit0;  // first unit of this item in the launch
+    uint32_t nchunk; // chunks of this row's list (an upper bound for tree rows)
+    uint32_t chunk;  // list entries per chunk (multiple of BLK)
+    uint64_t kvoff;  // slot offset of the row's cache (ragged pools), else 0
+};
+
+struct DirectParams {
+    const float* q;
+    const void* kc;
+    const void* vc;
+    float* out;
+    float* part_o;  // [unit][16][HD]
+    float* part_ml; // [unit][16][2]
+    const uint32_t* masks; // tree: two words per row
+    uint32_t nh, nkv, hd, G;
+    uint32_t base;  // tree: first tree slot
+    uint32_t tree;
+    uint64_t slot_limit; // slots the caches hold (tree slots past it read as absent)
+    float sc;       // scale * log2(e)
+    uint32_t split; // 1: a unit is one chunk of one item, written as a partial
+    uint32_t nitems;
+    Item items[MAX_ITEMS];
+};
+
+// Multi-row line attention: a workgroup takes rb rows x all G heads of one KV head.
+struct SharedParams {
+    const float* q;
+    const void* kc;
+    const void* vc;
+    float* out;
+    float* part_o;  // [unit][SL][HD]
+    float* part_ml; // [unit][SL][2]
+    uint32_t rows, nh, nkv, hd, G;
+    uint32_t pos;   // slot of row 0
+    float sc;
+    uint32_t rb;    // rows per workgroup
+    uint32_t nrb;   // row blocks
+    uint32_t nchunk;// chunks of the longest list (split launches)
+    uint32_t split;
+};
+
+struct CombineParams {
+    float* out;
+    const float* part_o;
+    const float* part_ml;
+    uint32_t nh, nkv, hd, G;
+    uint32_t slots;   // partial slots per unit (16 for direct, SL for shared)
+    // direct: one group per (item, kvh); shared: one group per (kvh, row block)
+    uint32_t shared;
+    uint32_t rows, rb, nrb, nchunk; // shared
+    uint32_t nitems;
+    Item items[MAX_ITEMS];
+};
+
+}  // namespace bchip

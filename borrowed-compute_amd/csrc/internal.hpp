@@ -1,0 +1,50 @@
+// Internal interface between the C ABI (bchip.hip) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace bchip {
+
+// Device scratch for split-K partials, owned by a context and grown on demand.
+struct Workspace {
+    float* o = nullptr;   // [units*slots][hd_pad]
+    float* ml = nullptr;  // [units*slots][2]
+    size_t slots = 0, hdp = 0;
+    hipError_t reserve(size_t need_slots, size_t hd_pad);
+    void release();
+};
+
+struct AttnCall {
+    const float* q;
+    const void* kc;
+    const void* vc;
+    uint32_t kv_type;  // 0 f32, 1 f16
+    float* out;
+    const uint32_t* masks;
+    uint32_t tree, rows, nh, nkv, hd, pos;
+    float scale;
+    uint64_t slot_limit;  // slots both caches hold (all slots a call may read when unknown)
+};
+
+uint32_t decode_chunk(uint64_t len);
+hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
+                            Workspace& ws, hipStream_t s);
+hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s);
+
+hipError_t rope_launch(float* x, const float* inv_freq, const uint32_t* positions, uint32_t rows,
+                       uint32_t heads, uint32_t hd, uint32_t rope_dim, uint32_t neox, hipStream_t s);
+hipError_t rope_append_launch(float* q, const float* k, const float* v, void* kc, void* vc, uint32_t kv_type,
+                              const float* inv_freq, const uint32_t* positions, uint32_t rows, uint32_t nh,
+                              uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint64_t slot0,
+                              hipStream_t s);
+hipError_t copy_launch(const void* src, uint32_t st, void* dst, uint32_t dt, uint64_t off, uint64_t n, hipStream_t s);
+hipError_t move_launch(void* buf, uint32_t type, uint64_t from, uint64_t to, uint64_t n, hipStream_t s);
+hipError_t keep_launch(void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width, uint64_t base,
+                       const uint32_t* rows, uint32_t nrows, hipStream_t s);
+hipError_t fill_normal_launch(void* dst, uint32_t type, uint64_t n, uint64_t seed, hipStream_t s);
+
+}  // namespace bchip

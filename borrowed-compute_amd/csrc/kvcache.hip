@@ -1,0 +1,138 @@
+// KV-cache movement: bc-infer's k_copy and k_move (crates/bc-infer/src/gpu/kernels.h:332-334,
+// entries cuda.cu:89-90), f16-aware, plus Cache::keep for every layer in one launch
+// (gpu/mod.rs:322-337), and the seeded N(0,1) generator of the benchmark inputs.
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+namespace bchip {
+
+template <typename S, typename D>
+__device__ __forceinline__ D conv(S v) {
+    return (D)v;
+}
+
+template <typename S, typename D>
+__global__ __launch_bounds__(256) void k_copy(const S* __restrict__ src, D* __restrict__ dst, uint64_t off,
+                                              uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[off + i] = conv<S, D>(src[i]);
+}
+
+// One element per thread; ranges of one launch never overlap (move_launch cuts them).
+template <typename T>
+__global__ __launch_bounds__(256) void k_move(T* b, uint64_t from, uint64_t to, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        b[to + i] = b[from + i];
+}
+
+struct KeepArgs {
+    void* bufs[64];
+    uint32_t rows[64];
+};
+
+// Each thread owns one element column of one buffer and applies the moves in ascending
+// order, as Kv::keep does (model.rs:158-161). Move i reads row base+rows[i] and writes row
+// base+i; a later move j > i writes row base+j, which may be a row a move before it read
+// (rows[i] = j), so the order matters and is kept per column.
+template <typename T>
+__global__ __launch_bounds__(256) void k_keep(const KeepArgs a, uint32_t nbufs, uint32_t width, uint64_t base,
+                                              uint32_t nrows) {
+    const uint32_t col = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t bi = blockIdx.y;
+    if (col >= width || bi >= nbufs) return;
+    T* b = (T*)a.bufs[bi];
+    for (uint32_t i = 0; i < nrows; i++) {
+        const uint32_t r = a.rows[i];
+        if (r != i) b[(base + i) * width + col] = b[(base + r) * width + col];
+    }
+}
+
+__device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t k) {
+    // Output k (from 0) of the sequence whose state starts at seed.
+    uint64_t z = seed + (k + 1) * 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_fill_normal(T* __restrict__ dst, uint64_t n, uint64_t seed) {
+    const double two_pi = 6.283185307179586476925286766559;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        double u1 = ((double)(splitmix64_at(seed, 2 * i) >> 11) + 1.0) * 0x1.0p-53;
+        double u2 = (double)(splitmix64_at(seed, 2 * i + 1) >> 11) * 0x1.0p-53;
+        double r = sqrt(-2.0 * log(u1));
+        dst[2 * i] = (T)(float)(r * cos(two_pi * u2));
+        if (2 * i + 1 < n) dst[2 * i + 1] = (T)(float)(r * sin(two_pi * u2));
+    }
+}
+
+static uint32_t grid_of(uint64_t n) {
+    uint64_t b = (n + 255) / 256;
+    return (uint32_t)(b > 65536 ? 65536 : (b ? b : 1));
+}
+
+hipError_t copy_launch(const void* src, uint32_t st, void* dst, uint32_t dt, uint64_t off, uint64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    dim3 g(grid_of(n)), b(256);
+    if (st == 0 && dt == 0)
+        hipLaunchKernelGGL((k_copy<float, float>), g, b, 0, s, (const float*)src, (float*)dst, off, n);
+    else if (st == 0 && dt == 1)
+        hipLaunchKernelGGL((k_copy<float, f16>), g, b, 0, s, (const float*)src, (f16*)dst, off, n);
+    else if (st == 1 && dt == 0)
+        hipLaunchKernelGGL((k_copy<f16, float>), g, b, 0, s, (const f16*)src, (float*)dst, off, n);
+    else
+        hipLaunchKernelGGL((k_copy<f16, f16>), g, b, 0, s, (const f16*)src, (f16*)dst, off, n);
+    return hipGetLastError();
+}
+
+hipError_t move_launch(void* buf, uint32_t type, uint64_t from, uint64_t to, uint64_t n, hipStream_t s) {
+    if (n == 0 || from == to) return hipSuccess;
+    // With from - to < n the ranges overlap: move in pieces of from - to, in order; each
+    // piece's source lies past its destination, and the pieces run one after another.
+    const uint64_t step = (from - to < n) ? from - to : n;
+    for (uint64_t o = 0; o < n; o += step) {
+        const uint64_t m = (n - o < step) ? n - o : step;
+        if (type == 1)
+            hipLaunchKernelGGL(k_move<f16>, dim3(grid_of(m)), dim3(256), 0, s, (f16*)buf, from + o, to + o, m);
+        else
+            hipLaunchKernelGGL(k_move<float>, dim3(grid_of(m)), dim3(256), 0, s, (float*)buf, from + o, to + o, m);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t keep_launch(void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width, uint64_t base,
+                       const uint32_t* rows, uint32_t nrows, hipStream_t s) {
+    if (nbufs == 0 || nrows == 0 || width == 0) return hipSuccess;
+    for (uint32_t b0 = 0; b0 < nbufs; b0 += 64) {
+        KeepArgs a{};
+        const uint32_t nb = (nbufs - b0 < 64) ? nbufs - b0 : 64;
+        for (uint32_t i = 0; i < nb; i++) a.bufs[i] = bufs[b0 + i];
+        for (uint32_t i = 0; i < nrows; i++) a.rows[i] = rows[i];
+        dim3 g((width + 255) / 256, nb);
+        if (type == 1)
+            hipLaunchKernelGGL(k_keep<f16>, g, dim3(256), 0, s, a, nb, width, base, nrows);
+        else
+            hipLaunchKernelGGL(k_keep<float>, g, dim3(256), 0, s, a, nb, width, base, nrows);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t fill_normal_launch(void* dst, uint32_t type, uint64_t n, uint64_t seed, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const uint64_t pairs = (n + 1) / 2;
+    if (type == 1)
+        hipLaunchKernelGGL(k_fill_normal<f16>, dim3(grid_of(pairs)), dim3(256), 0, s, (f16*)dst, n, seed);
+    else
+        hipLaunchKernelGGL(k_fill_normal<float>, dim3(grid_of(pairs)), dim3(256), 0, s, (float*)dst, n, seed);
+    return hipGetLastError();
+}
+
+}  // namespace bchip

@@ -1,0 +1,155 @@
+/* bchip: bc-infer's attention path on one AMD Instinct MI355X (gfx950), as a C ABI.
+ *
+ * This is the boundary a `gpu/hip.rs` backend binds in place of `gpu/cuda.rs`
+ * (crates/bc-infer/src/gpu/cuda.rs:1-95) for the attention sub-sequence of
+ * `Layers::forward` (crates/bc-infer/src/gpu/mod.rs:464-482), `Cache::keep`
+ * (mod.rs:322-337) and `Layers::reserve` (mod.rs:404-423). Plain pointers and sizes only.
+ *
+ * Conventions
+ *  - Every call returns an int: BCHIP_OK (0) or a negative BCHIP_E_* code; the message of
+ *    the last failing call on this thread is bchip_last_error(). Nothing aborts or throws
+ *    across the ABI (the reference maps failures to anyhow::Result, gpu/mod.rs:119-134).
+ *  - "Device pointer" arguments are addresses in the context's device memory, from
+ *    bchip_alloc or any other allocator on that device. Host pointers are only read or
+ *    written during the call.
+ *  - All kernels run in order on the context's one stream (cuda.rs:40, one stream);
+ *    launches return before the work ends; bchip_sync waits (cuda.rs:93). The caller
+ *    serialises calls on one context, as the reference's Gpu mutex does (mod.rs:105-107).
+ *  - Element types of cache buffers: BCHIP_F32 (the reference's f32 cache, mod.rs:409-421)
+ *    or BCHIP_F16 (IEEE binary16, rounded to nearest even: new with this backend).
+ *  - Cache layout is the reference's: per layer, K and V each [slots][n_head_kv*head_dim]
+ *    (slot t of KV head h at t*kvd + h*head_dim, mod.rs:473-475, kernels.h:287,310).
+ */
+#ifndef BCHIP_H
+#define BCHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BCHIP_ABI_VERSION 1
+
+enum bchip_type { BCHIP_F32 = 0, BCHIP_F16 = 1 }; /* T_F32 / T_F16 of kernels.h:14-15 */
+
+enum bchip_status {
+    BCHIP_OK = 0,
+    BCHIP_E_ARG = -1,         /* an argument is out of range or inconsistent */
+    BCHIP_E_HIP = -2,         /* the HIP runtime reported an error */
+    BCHIP_E_NODEV = -3,       /* no usable gfx950 device */
+    BCHIP_E_DISABLED = -4,    /* BC_INFER_GPU=0 in the environment (mod.rs:116) */
+    BCHIP_E_UNSUPPORTED = -5, /* a shape this backend does not take */
+    BCHIP_E_OOM = -6          /* device memory exhausted */
+};
+
+typedef struct bchip_ctx bchip_ctx;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* bchip_last_error(void);
+int bchip_abi_version(void);
+
+/* Backend::new (cuda.rs:32-42): opens `device`, checks it is gfx950, creates the stream.
+ * Fails with BCHIP_E_DISABLED when BC_INFER_GPU=0 (gpu/mod.rs:116). */
+int bchip_init(int device, bchip_ctx** ctx);
+int bchip_destroy(bchip_ctx* ctx);
+
+/* Backend::name (cuda.rs:44-46): NUL-terminated, truncated to len. */
+int bchip_device_name(bchip_ctx* ctx, char* buf, size_t len);
+/* Backend::memory (cuda.rs:49-51): free device bytes now. */
+int bchip_mem_free(bchip_ctx* ctx, uint64_t* free_bytes);
+/* Backend::unified (cuda.rs:53-55): 0, memory is the card's own. */
+int bchip_unified(bchip_ctx* ctx, int* unified);
+
+/* Backend::zeros (cuda.rs:66-68): `bytes` of zeroed device memory (at least 1). */
+int bchip_alloc(bchip_ctx* ctx, size_t bytes, void** dev);
+/* Drop of a Buf (cudarc frees on drop). */
+int bchip_free(bchip_ctx* ctx, void* dev);
+/* Backend::upload / weights (cuda.rs:57-64): host -> dev+off, synchronous. */
+int bchip_upload(bchip_ctx* ctx, void* dev, size_t off, const void* host, size_t bytes);
+/* Backend::read (cuda.rs:70-76): dev+off -> host after all queued work, synchronous. */
+int bchip_download(bchip_ctx* ctx, const void* dev, size_t off, void* host, size_t bytes);
+/* The wait at the end of Backend::run (cuda.rs:93). */
+int bchip_sync(bchip_ctx* ctx);
+/* The context's hipStream_t (for callers that time or order their own work on it). */
+int bchip_stream(bchip_ctx* ctx, void** hip_stream);
+
+/* k_rope (kernels.h:237-248, entry cuda.cu:81; launched at mod.rs:464-472): rotates, in
+ * place, pair i of every head of row r of x [rows][heads][hd] (f32) by
+ * positions[r] * inv_freq[i]; neox pairs (i, i + rope_dim/2), else (2i, 2i+1).
+ * positions: device u32 [rows]; inv_freq: device f32 [rope_dim/2]. */
+int bchip_rope(bchip_ctx* ctx, float* x, const float* inv_freq, const uint32_t* positions,
+               uint32_t rows, uint32_t heads, uint32_t hd, uint32_t rope_dim, uint32_t neox);
+
+/* k_copy (kernels.h:332, entry cuda.cu:90; mod.rs:413-420, 473-475):
+ * dst[dst_off + i] = src[i] for i < n (element offsets and counts), converting from
+ * src_type to dst_type (f32 -> f16 rounds to nearest even). */
+int bchip_copy(bchip_ctx* ctx, const void* src, uint32_t src_type, void* dst,
+               uint32_t dst_type, uint64_t dst_off, uint64_t n);
+
+/* k_move (kernels.h:334, entry cuda.cu:89): within one buffer, b[to + i] = b[from + i]
+ * for i < n elements, to <= from; overlapping ranges are handled. */
+int bchip_move(bchip_ctx* ctx, void* buf, uint32_t type, uint64_t from, uint64_t to, uint64_t n);
+
+/* Cache::keep (mod.rs:322-337) for `nbufs` cache buffers at once (every layer's K and V):
+ * row base+rows[i] moves to base+i for each i with rows[i] != i, in order. rows (host) must
+ * ascend (Kv::keep's check, model.rs:147); nrows <= 64. width = n_head_kv * head_dim.
+ * bufs is a host array of device pointers. */
+int bchip_keep(bchip_ctx* ctx, void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width,
+               uint64_t base, const uint32_t* rows, uint32_t nrows);
+
+/* The attention sub-sequence k_rope(q), k_rope(k), k_copy(k -> kc), k_copy(v -> vc)
+ * (mod.rs:464-475) as one launch: rotates q [rows][nh][hd] in place, rotates k
+ * [rows][nkv][hd] and writes it, with v [rows][nkv][hd], into cache slots slot0 + r of
+ * kc and vc (type kv_type). k and v (f32) are read only. positions as bchip_rope. */
+int bchip_rope_append(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
+                      uint32_t kv_type, const float* inv_freq, const uint32_t* positions,
+                      uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim,
+                      uint32_t neox, uint64_t slot0);
+
+/* k_attention (kernels.h:250-324, entry cuda.cu:82-85; launched at mod.rs:476-482):
+ * causal grouped-query attention of `rows` rows. q, out: device f32 [rows][nh][hd];
+ * kc, vc: cache of kv_type; head h reads KV head h / (nh/nkv).
+ *  - tree == 0 (a line): row r sees slots 0 .. pos + r.
+ *  - tree != 0: pos is the tree's first slot; row r sees slots 0 .. pos-1 and the slots
+ *    pos + j for each set bit j of its 64-bit mask, masks[2r] (bits 0-31) and
+ *    masks[2r+1] (bits 32-63) (device u32 [2*rows], mod.rs:436-442), summed in list order:
+ *    the k-th entry of the list is slot k below pos, then the (k-pos)-th set bit
+ *    (kernels.h:266-278), so a tree row gets exactly the bits of the line its path is.
+ * Requires hd % 8 == 0, hd <= 256, nh % nkv == 0, nh/nkv <= 16.
+ * Every row of a multi-row call (rows >= 2) is computed by the same fixed-order
+ * arithmetic, which depends only on the row's q and its visible slot list: results are
+ * identical whatever the batch, the row's index, or whether it is a tree node or a line
+ * token. A one-row call computes in the same order, with chunks sized by its length
+ * (identical to a batch row from 16384 visible slots up, otherwise within rounding). */
+int bchip_attention(bchip_ctx* ctx, const float* q, const void* kc, const void* vc,
+                    uint32_t kv_type, float* out, const uint32_t* masks, uint32_t tree,
+                    uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t pos,
+                    float scale);
+
+/* Several conversations' one-token steps in one launch (the reference runs one
+ * k_attention per KV stream, crates/bc-mesh/src/engine.rs:25,305-309): sequence i's row
+ * q[i] [nh][hd] sees the seq_lens[i] slots kv_offsets[i] .. kv_offsets[i]+seq_lens[i]-1 of
+ * the shared kc/vc pool (a ragged layout). Each sequence's result equals bchip_attention
+ * with rows = 1, pos = seq_lens[i]-1 on its own slots, bit for bit. seq_lens and
+ * kv_offsets are host arrays; nseq <= 256. */
+int bchip_attention_ragged(bchip_ctx* ctx, const float* q, const void* kc, const void* vc,
+                           uint32_t kv_type, float* out, const uint32_t* seq_lens,
+                           const uint64_t* kv_offsets, uint32_t nseq, uint32_t nh,
+                           uint32_t nkv, uint32_t hd, float scale);
+
+/* Seeded N(0,1) draws into dst (n elements of type): splitmix64 (Steele, Lea and Flood
+ * 2014) + Box-Muller (1958), the generator of the benchmark inputs; draw i of seed s is
+ * the oracle's draw i of s up to the last bit of the device's log/sin/cos. */
+int bchip_fill_normal(bchip_ctx* ctx, void* dst, uint32_t type, uint64_t n, uint64_t seed);
+
+/* Timing on the context's stream: start records an event; stop records another, waits
+ * for it and returns the milliseconds between them. */
+int bchip_timer_start(bchip_ctx* ctx);
+int bchip_timer_stop(bchip_ctx* ctx, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
