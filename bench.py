@@ -1,0 +1,377 @@
+"""Benchmark of the MI355X attention path (libbchip.so) on BASELINE.json's configurations.
+
+Headline (`value`): configs[1], Llama-3-8B-shaped decode: batch 1, 32 query / 8 KV heads,
+head_dim 128, f16 KV cache at 32768 visible slots, RoPE theta 5e5 fused with the one-row
+K/V append, 32 layers with distinct caches. A step is one token through all 32 layers
+(bchip_rope_append + bchip_attention per layer); value = tokens/s of those steps, with
+inputs resident in HBM. Extras: decode at 1024 and 4096 slots (their 32 layers' caches fit
+the 256 MB MALL: labelled so), causal prefill at 2048 and 8192 tokens (TFLOP/s, configs[2]),
+the Llama-3-70B stage share's verify steps, Qwen2.5-7B ragged batched decode
+(configs[3]).
+
+roofline: the decode attention kernel's algorithmic bytes per launch (2 * L * n_kv * hd * 2
+bytes of f16 K and V, each read once) over its mean launch time, from HIP events recorded
+around every attention launch of the timed region on the library's stream.
+
+cpu_baseline: bc-infer's CPU attention as the oracle's C restatement (single thread, as
+the reference runs it: crates/bc-infer/src/model.rs:391-403, 448-481), timed on this
+host on a bounded sample of the same workload: a few layers of one decode token at 32768
+slots, median per layer, scaled to tokens/s for 32 layers.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "borrowed-compute_amd"))
+
+import numpy as np  # noqa: E402
+
+import bchip  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2516.6
+METRIC = "attn decode GB/s & prefill TFLOP/s on 1 MI355X, % of roofline; tokens/s"
+
+
+class Hip:
+    """hipEvent timing on a given stream (the library's), through the HIP runtime."""
+
+    def __init__(self):
+        path = None
+        for cand in ("/opt/rocm/lib/libamdhip64.so", "libamdhip64.so"):
+            try:
+                self.lib = ctypes.CDLL(cand)
+                path = cand
+                break
+            except OSError:
+                continue
+        if path is None:
+            raise RuntimeError("libamdhip64.so not found")
+        L = self.lib
+        L.hipEventCreate.argtypes = [ctypes.c_void_p]
+        L.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        L.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        L.hipEventElapsedTime.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def events(self, n):
+        out = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            assert self.lib.hipEventCreate(ctypes.byref(e)) == 0
+            out.append(e.value)
+        return out
+
+    def record(self, e, stream):
+        assert self.lib.hipEventRecord(e, stream) == 0
+
+    def elapsed(self, a, b):
+        assert self.lib.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.lib.hipEventDestroy(e)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class DecodeModel:
+    """n_layer layers' caches and per-step inputs on the device, all generated there."""
+
+    def __init__(self, ctx, nh, nkv, hd, theta, neox, n_layer, ctx_len, steps, seed=1):
+        self.ctx, self.nh, self.nkv, self.hd, self.n_layer = ctx, nh, nkv, hd, n_layer
+        self.ctx_len, self.steps = ctx_len, steps
+        kvd = nkv * hd
+        cap = ctx_len + steps + 1
+        self.kc, self.vc = [], []
+        for layer in range(n_layer):
+            k = ctx.zeros(cap * kvd * 2)
+            v = ctx.zeros(cap * kvd * 2)
+            ctx.fill_normal(k, bchip.F16, ctx_len * kvd, seed * 1000 + 2 * layer)
+            ctx.fill_normal(v, bchip.F16, ctx_len * kvd, seed * 1000 + 2 * layer + 1)
+            self.kc.append(k)
+            self.vc.append(v)
+        # q, k, v of every (step, layer), positions of every step.
+        per = (nh + 2 * nkv) * hd
+        self.qkv = ctx.zeros(steps * n_layer * per * 4)
+        ctx.fill_normal(self.qkv, bchip.F32, steps * n_layer * per, seed * 7919)
+        self.out = ctx.zeros(nh * hd * 4)
+        self.pos = ctx.upload(np.arange(ctx_len, ctx_len + steps, dtype=np.uint32))
+        inv = np.array([theta ** (-2.0 * i / hd) for i in range(hd // 2)], np.float32)
+        self.inv = ctx.upload(inv)
+        self.neox = neox
+        self.per = per
+        ctx.sync()
+
+    def layer_ptrs(self, step, layer):
+        base = self.qkv.ptr + (step * self.n_layer + layer) * self.per * 4
+        q = base
+        k = base + self.nh * self.hd * 4
+        v = k + self.nkv * self.hd * 4
+        return q, k, v
+
+    def step(self, step, hip=None, evs=None):
+        ctx = self.ctx
+        slot = self.ctx_len + step
+        for layer in range(self.n_layer):
+            q, k, v = self.layer_ptrs(step, layer)
+            ctx.rope_append(q, k, v, self.kc[layer], self.vc[layer], bchip.F16, self.inv, self.pos.ptr + 4 * step, 1,
+                            self.nh, self.nkv, self.hd, self.hd, self.neox, slot)
+            if evs is not None:
+                hip.record(evs[2 * layer], self.stream)
+            ctx.attention(q, self.kc[layer], self.vc[layer], bchip.F16, self.out, None, False, 1, self.nh, self.nkv,
+                          self.hd, slot, 1.0 / math.sqrt(self.hd))
+            if evs is not None:
+                hip.record(evs[2 * layer + 1], self.stream)
+
+    def free(self):
+        for b in self.kc + self.vc + [self.qkv, self.out, self.pos, self.inv]:
+            b.free()
+
+
+def bench_decode(ctx, hip, ctx_len, steps, warmup, n_layer=32, nh=32, nkv=8, hd=128, theta=5e5, neox=False):
+    m = DecodeModel(ctx, nh, nkv, hd, theta, neox, n_layer, ctx_len, steps + warmup)
+    m.stream = ctx.stream()
+    for s in range(warmup):
+        m.step(s)
+    ctx.sync()
+    evs = hip.events(2 * n_layer * steps)
+    ctx.timer_start()
+    for s in range(steps):
+        m.step(warmup + s, hip, evs[2 * n_layer * s: 2 * n_layer * (s + 1)])
+    total_ms = ctx.timer_stop()
+    kernel_ms = [hip.elapsed(evs[2 * i], evs[2 * i + 1]) for i in range(n_layer * steps)]
+    hip.destroy(evs)
+    m.free()
+    mean_kernel_ms = statistics.fmean(kernel_ms)
+    # Visible slots grow by one per step: average algorithmic bytes over the timed launches.
+    mean_len = ctx_len + warmup + (steps - 1) / 2 + 1
+    bytes_per_launch = 2 * mean_len * nkv * hd * 2
+    gbs = bytes_per_launch / (mean_kernel_ms * 1e-3) / 1e9
+    return {
+        "ctx": ctx_len, "layers": n_layer, "steps": steps, "ms_per_step": total_ms / steps,
+        "tokens_per_s": steps / (total_ms * 1e-3), "attn_launch_us": mean_kernel_ms * 1e3,
+        "attn_bytes_per_launch": bytes_per_launch, "attn_GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+    }
+
+
+def bench_multirow(ctx, hip, rows, pos, nh, nkv, hd, reps, n_layer=1, verify=False):
+    """Causal multi-row attention over n_layer distinct caches (prefill: pos 0)."""
+    kvd = nkv * hd
+    slots = pos + rows
+    kcs, vcs = [], []
+    for layer in range(n_layer):
+        k, v = ctx.zeros(slots * kvd * 2), ctx.zeros(slots * kvd * 2)
+        ctx.fill_normal(k, bchip.F16, slots * kvd, 50 + 2 * layer)
+        ctx.fill_normal(v, bchip.F16, slots * kvd, 51 + 2 * layer)
+        kcs.append(k)
+        vcs.append(v)
+    q = ctx.zeros(rows * nh * hd * 4)
+    ctx.fill_normal(q, bchip.F32, rows * nh * hd, 49)
+    out = ctx.zeros(rows * nh * hd * 4)
+    stream = ctx.stream()
+    scale = 1.0 / math.sqrt(hd)
+    for layer in range(n_layer):
+        ctx.attention(q, kcs[layer], vcs[layer], bchip.F16, out, None, False, rows, nh, nkv, hd, pos, scale)
+    ctx.sync()
+    evs = hip.events(2 * reps * n_layer)
+    i = 0
+    ctx.timer_start()
+    for r in range(reps):
+        for layer in range(n_layer):
+            hip.record(evs[i], stream)
+            ctx.attention(q, kcs[layer], vcs[layer], bchip.F16, out, None, False, rows, nh, nkv, hd, pos, scale)
+            hip.record(evs[i + 1], stream)
+            i += 2
+    total_ms = ctx.timer_stop()
+    per = [hip.elapsed(evs[2 * j], evs[2 * j + 1]) for j in range(reps * n_layer)]
+    hip.destroy(evs)
+    for b in kcs + vcs + [q, out]:
+        b.free()
+    pairs = rows * pos + rows * (rows + 1) / 2  # unmasked (query, key) pairs
+    flops = 4.0 * hd * nh * pairs
+    kv_bytes = 2.0 * slots * kvd * 2
+    us = statistics.fmean(per) * 1e3
+    res = {"rows": rows, "pos": pos, "heads": [nh, nkv, hd], "layers": n_layer, "launch_us": us,
+           "ms_per_pass": total_ms / reps, "TFLOPs": flops / (us * 1e-6) / 1e12,
+           "mfma_frac": flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS}
+    if verify:
+        res["GBps"] = kv_bytes / (us * 1e-6) / 1e9
+        res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
+    return res
+
+
+def bench_ragged(ctx, hip, reps):
+    """16 sequences, lengths U[1024, 32768] (seeded), 28/4 heads, hd 128, one
+    launch per layer over a ragged pool, 28 layers."""
+    nh, nkv, hd, n_layer = 28, 4, 128, 28
+    rng = np.random.default_rng(4)
+    lens = rng.integers(1024, 32769, size=16).astype(np.uint32)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    total = int(lens.sum())
+    kvd = nkv * hd
+    kcs, vcs = [], []
+    for layer in range(n_layer):
+        k, v = ctx.zeros(total * kvd * 2), ctx.zeros(total * kvd * 2)
+        ctx.fill_normal(k, bchip.F16, total * kvd, 300 + 2 * layer)
+        ctx.fill_normal(v, bchip.F16, total * kvd, 301 + 2 * layer)
+        kcs.append(k)
+        vcs.append(v)
+    q = ctx.zeros(16 * nh * hd * 4)
+    ctx.fill_normal(q, bchip.F32, 16 * nh * hd, 299)
+    out = ctx.zeros(16 * nh * hd * 4)
+    stream = ctx.stream()
+    for layer in range(n_layer):
+        ctx.attention_ragged(q, kcs[layer], vcs[layer], bchip.F16, out, lens, offs, nh, nkv, hd, 0.0884)
+    ctx.sync()
+    evs = hip.events(2 * reps * n_layer)
+    i = 0
+    ctx.timer_start()
+    for r in range(reps):
+        for layer in range(n_layer):
+            hip.record(evs[i], stream)
+            ctx.attention_ragged(q, kcs[layer], vcs[layer], bchip.F16, out, lens, offs, nh, nkv, hd, 0.0884)
+            hip.record(evs[i + 1], stream)
+            i += 2
+    total_ms = ctx.timer_stop()
+    per = [hip.elapsed(evs[2 * j], evs[2 * j + 1]) for j in range(reps * n_layer)]
+    hip.destroy(evs)
+    for b in kcs + vcs + [q, out]:
+        b.free()
+    us = statistics.fmean(per) * 1e3
+    bytes_ = 2.0 * total * kvd * 2
+    return {"seqs": 16, "total_slots": total, "layers": n_layer, "launch_us": us, "ms_per_step": total_ms / reps,
+            "tokens_per_s": 16 * reps / (total_ms * 1e-3), "GBps": bytes_ / (us * 1e-6) / 1e9,
+            "hbm_frac": bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+def cpu_baseline(layers=5, ctx_len=32768, nh=32, nkv=8, hd=128):
+    """The oracle's single-thread attention (+ rope of the new q and k rows) per layer of one
+    decode token at ctx_len slots; median over `layers` layers, scaled to 32 layers."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    O.lib()
+    inv = O.inv_freq(hd, 5e5)
+    times = []
+    for layer in range(layers):
+        q = O.normal(10 + layer, nh * hd).reshape(1, nh, hd)
+        kc = O.normal(20 + layer, (ctx_len + 1) * nkv * hd).reshape(ctx_len + 1, nkv * hd)
+        vc = O.normal(30 + layer, (ctx_len + 1) * nkv * hd).reshape(ctx_len + 1, nkv * hd)
+        t0 = time.perf_counter()
+        qr = O.rope(q, nh, hd, hd, False, ctx_len, inv)
+        kc[ctx_len] = O.rope(kc[ctx_len], nkv, hd, hd, False, ctx_len, inv)
+        O.attention(qr, kc, vc, 1, ctx_len, nh, nkv, hd, 1.0 / math.sqrt(hd))
+        times.append(time.perf_counter() - t0)
+    per_layer = statistics.median(times)
+    return {"value": 1.0 / (32 * per_layer), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{layers} layers of one Llama-3-8B decode token at {ctx_len} slots (f32 oracle, "
+                      f"model.rs:391-403+448-481 restated in C, 1 thread); median {per_layer * 1e3:.1f} ms/layer, "
+                      f"scaled to 32 layers",
+            "cpu": _cpu_model(), "nproc": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ctx", type=int, default=32768, help="visible slots of the headline decode")
+    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,ragged,cpu")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": f"--gpus {args.gpus}: this build runs on one GPU; the attention path's "
+                                   "multi-GPU sharding is described in DESIGN.md, not run"}))
+        sys.exit(2)
+    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "ragged", "cpu"}
+    hip = Hip()
+    extra = {}
+    with bchip.Ctx(0) as ctx:
+        log(f"device: {ctx.name()}")
+        head = None
+        if "decode" in want:
+            log(f"decode: 32 layers at {args.ctx} slots, {args.warmup}+{args.steps} steps")
+            head = bench_decode(ctx, hip, args.ctx, args.steps, args.warmup)
+            log(json.dumps(head))
+        if "short" in want:
+            for L in (1024, 4096):
+                log(f"decode at {L} slots (all 32 layers' caches fit the 256 MB MALL)")
+                r = bench_decode(ctx, hip, L, args.steps, args.warmup)
+                r["note"] = "MALL-resident and launch-bound: reported, not a roofline figure"
+                extra[f"decode_{L}"] = r
+                log(json.dumps(r))
+        if "prefill" in want:
+            for S, layers, reps in ((2048, 32, 2), (8192, 4, 2)):
+                log(f"prefill {S} tokens, {layers} layers x {reps}")
+                r = bench_multirow(ctx, hip, S, 0, 32, 8, 128, reps, n_layer=layers)
+                extra[f"prefill_{S}"] = r
+                log(json.dumps(r))
+        if "verify" in want:
+            log("Llama-3-70B share: 4096-token prefill, verify 8 rows at 4096 and 6136 slots, 20 layers")
+            extra["prefill_70b_4096"] = bench_multirow(ctx, hip, 4096, 0, 64, 8, 128, 1, n_layer=20)
+            log(json.dumps(extra["prefill_70b_4096"]))
+            for ctx_len in (4096, 6136):
+                r = bench_multirow(ctx, hip, 8, ctx_len, 64, 8, 128, 10, n_layer=20, verify=True)
+                extra[f"verify_70b_{ctx_len}"] = r
+                log(json.dumps(r))
+        if "ragged" in want:
+            log("ragged: 16 Qwen2.5-7B sequences, 28 layers")
+            extra["ragged_qwen7b"] = bench_ragged(ctx, hip, 5)
+            log(json.dumps(extra["ragged_qwen7b"]))
+    cpu = None
+    if "cpu" in want:
+        log("cpu baseline (oracle, 1 thread)")
+        cpu = cpu_baseline()
+        log(json.dumps(cpu))
+    if head is None:
+        print(json.dumps({"extra": extra, "cpu_baseline": cpu}))
+        return
+    line = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: seeded N(0,1) q/k/v and KV cache (splitmix64 + Box-Muller, generated on the device)",
+        "config": {"workload": "configs[1]: Llama-3-8B decode attention, batch 1, 32/8 heads, head_dim 128, "
+                               f"f16 KV at {args.ctx} slots, RoPE theta 5e5 fused with the K/V append, 32 layers",
+                   "ctx": args.ctx, "layers": 32},
+        "roofline": {"bound": "hbm", "achieved": head["attn_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["hbm_frac"], "traffic": None,
+                     "kernel": "bchip attention (rows=1 decode)",
+                     "bytes_per_launch": head["attn_bytes_per_launch"], "launch_us": head["attn_launch_us"]},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

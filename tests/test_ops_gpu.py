@@ -84,7 +84,7 @@ def test_copy_converts_and_offsets(ctx):
         np.testing.assert_array_equal(got[150:1150], x.astype(npt))
         assert not got[:150].any() and not got[1150:].any()
         back = ctx.zeros(4000)
-        ctx.copy(dst, dt, back, bchip.F32, 0, 1000)
+        ctx.copy(dst.ptr + 150 * bchip.esize(dt), dt, back, bchip.F32, 0, 1000)
         np.testing.assert_array_equal(ctx.read(back, 1000), x.astype(npt).astype(np.float32))
         dst.free()
         back.free()
