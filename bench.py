@@ -256,6 +256,23 @@ def bench_ragged(ctx, hip, reps):
             "hbm_frac": bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_copy_calibration(ctx, hip, mib=256, reps=4):
+    """A plain f16 copy of known size (bchip_copy): the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters of a profiling run, and achievable copy bandwidth."""
+    n = mib * 1024 * 1024 // 2
+    src, dst = ctx.zeros(n * 2), ctx.zeros(n * 2)
+    ctx.copy(src, bchip.F16, dst, bchip.F16, 0, n)
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(reps):
+        ctx.copy(src, bchip.F16, dst, bchip.F16, 0, n)
+    ms = ctx.timer_stop()
+    src.free()
+    dst.free()
+    return {"bytes_read_per_copy": n * 2, "bytes_written_per_copy": n * 2, "copies": reps + 1,
+            "copy_GBps": 2 * n * 2 * reps / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(layers=5, ctx_len=32768, nh=32, nkv=8, hd=128):
     """The oracle's single-thread attention (+ rope of the new q and k rows) per layer of one
     decode token at ctx_len slots; median over `layers` layers, scaled to 32 layers."""
@@ -298,13 +315,13 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ctx", type=int, default=32768, help="visible slots of the headline decode")
-    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,ragged,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,ragged,calib,cpu")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build runs on one GPU; the attention path's "
                                    "multi-GPU sharding is described in DESIGN.md, not run"}))
         sys.exit(2)
-    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "ragged", "cpu"}
+    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "ragged", "calib", "cpu"}
     hip = Hip()
     extra = {}
     with bchip.Ctx(0) as ctx:
@@ -335,6 +352,9 @@ def main():
                 r = bench_multirow(ctx, hip, 8, ctx_len, 64, 8, 128, 10, n_layer=20, verify=True)
                 extra[f"verify_70b_{ctx_len}"] = r
                 log(json.dumps(r))
+        if "calib" in want:
+            extra["copy_calibration"] = bench_copy_calibration(ctx, hip)
+            log(json.dumps(extra["copy_calibration"]))
         if "ragged" in want:
             log("ragged: 16 Qwen2.5-7B sequences, 28 layers")
             extra["ragged_qwen7b"] = bench_ragged(ctx, hip, 5)

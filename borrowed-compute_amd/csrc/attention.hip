@@ -13,17 +13,21 @@
 //                                   registers (the key order inside the MFMA k-dimension is
 //                                   chosen so), V^T is V transposed through LDS.
 // A row's list is cut into chunks; each chunk is an online softmax from a fresh state and
-// the row's result is the left fold of its chunks' (m, l, O) (merge below). The same code
-// computes every chunk, whichever workgroup runs it, so a chunk can run on any CU:
-//  - attn_direct: one wave, one tile = the G heads of one row; K straight from HBM into
-//    MFMA operands, V through a per-wave LDS tile. One-row decode (split across CUs by
-//    chunk), ragged multi-sequence decode, and tree rows (each row gathers its own list).
+// the row's result is the left fold of its chunks' (m, l, O) (merge below). The same
+// arithmetic computes every chunk, whichever workgroup runs it, so a chunk can run on any
+// CU and the row's bits do not change:
+//  - attn_decode: four waves split each block (wave w scores key tile w and owns hd slice
+//    w of the values), exchanging maxima, sums and P through LDS; the next block's K and V
+//    are in flight while one is computed. The G heads of one row per workgroup: one-row
+//    decode (split across CUs by chunk), ragged multi-sequence decode, and tree rows (each
+//    row gathers its own list).
 //  - attn_shared: four waves share K/V blocks staged in LDS (double-buffered) for up to
 //    128 slots (rows x G heads of one KV head): prefill and line verify.
-//  - attn_combine: the left fold of split chunks, in chunk order.
+//  - attn_combine: the left fold of split chunks, in chunk order; the fold weights depend
+//    only on the running maxima, so they are computed for all chunks at once (a prefix
+//    max), leaving a three-operation recurrence per output.
 // Every product of the fold, the softmax and the normalisation rounds on its own (the
-// library is built with -ffp-contract=off), so the fold is the same bits in a register
-// loop and in attn_combine.
+// library is built with -ffp-contract=off), so each step is the same bits in every kernel.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -34,16 +38,17 @@ namespace bchip {
 // f16 per row of the transposed V tile in LDS: 64 keys + 4 pad (8-byte aligned rows).
 constexpr int VTS = BLK + 4;
 
-template <int HD>
+// Softmax state of the lane's slot over NDT output tiles of 16 dims.
+template <int NDT>
 struct State {
-    f32x4 o[HD / 16];  // O^T[16*dt + 4*(lane/16) + i][lane%16]
-    float m, l;        // running max (log2 units) and sum of this lane's slot
+    f32x4 o[NDT];  // O^T[16*dt + 4*(lane/16) + i][lane%16]
+    float m, l;    // running max (log2 units) and sum
 };
 
-template <int HD>
-__device__ __forceinline__ void state_clear(State<HD>& s) {
+template <int NDT>
+__device__ __forceinline__ void state_clear(State<NDT>& s) {
 #pragma unroll
-    for (int i = 0; i < HD / 16; i++) s.o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < NDT; i++) s.o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     s.m = -INFINITY;
     s.l = 0.0f;
 }
@@ -60,15 +65,30 @@ __device__ __forceinline__ void merge_coef(float M, float m, float& a, float& b,
     b = exp2_hw(m - ms);
 }
 
-// R <- fold(R, c). The per-element expression is the one attn_combine uses.
-template <int HD>
-__device__ __forceinline__ void fold(State<HD>& R, const State<HD>& c) {
+// R <- fold(R, c). attn_combine applies the same per-element expression.
+template <int NDT>
+__device__ __forceinline__ void fold(State<NDT>& R, const State<NDT>& c) {
     float a, b, mn;
     merge_coef(R.m, c.m, a, b, mn);
     R.l = R.l * a + c.l * b;
 #pragma unroll
-    for (int i = 0; i < HD / 16; i++) R.o[i] = R.o[i] * a + c.o[i] * b;
+    for (int i = 0; i < NDT; i++) R.o[i] = R.o[i] * a + c.o[i] * b;
     R.m = mn;
+}
+
+// Sum of one slot's values over a 16-key tile: the lane's four keys in order, then the
+// four lane groups (l, l^16, l^32, l^48) pairwise. A block's sum adds the four tiles'
+// sums in tile order.
+__device__ __forceinline__ float tile_sum(float s) {
+    s = s + __shfl_xor(s, 16);
+    s = s + __shfl_xor(s, 32);
+    return s;
+}
+
+__device__ __forceinline__ float tile_max(float m) {
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    return m;
 }
 
 // The V^T operand of one PV MFMA: lane (g, n) holds V[key(g, j)][16*dt + n] for the
@@ -86,7 +106,7 @@ __device__ __forceinline__ half8 v_operand(const f16* __restrict__ vt, int dt, i
 // lane (g, n) holds K[key0 + 16kt + n][32c + 8g .. +8]. vt is V^T of the block in LDS.
 // len[t] is the list length of this lane's slot in tile t (entries >= len are masked).
 template <int HD, int NT, typename KOp>
-__device__ __forceinline__ void block_step(State<HD> (&s)[NT], const half8 (&qb)[NT][HD / 32], KOp kop,
+__device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 (&qb)[NT][HD / 32], KOp kop,
                                            const f16* __restrict__ vt, uint32_t key0,
                                            const uint32_t (&len)[NT], float sc) {
     const int lane = threadIdx.x & 63;
@@ -106,33 +126,35 @@ __device__ __forceinline__ void block_step(State<HD> (&s)[NT], const half8 (&qb)
     half8 pb[NT][2];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        float mx = -INFINITY;
         float x[4][4];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
+        for (int kt = 0; kt < 4; kt++) {
+            float tm = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 uint32_t k = key0 + 16 * kt + 4 * g + i;
                 float v = st[t][kt][i] * sc;
                 x[kt][i] = (k < len[t]) ? v : -INFINITY;
-                mx = fmaxf(mx, x[kt][i]);
+                tm = fmaxf(tm, x[kt][i]);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = fmaxf(mx, tile_max(tm));
+        }
         float mn = fmaxf(s[t].m, mx);
         float ms = (mn == -INFINITY) ? 0.0f : mn;
         float corr = exp2_hw(s[t].m - ms);
         float ps = 0.0f;
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
+        for (int kt = 0; kt < 4; kt++) {
+            float ts = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 f16 ph = (f16)exp2_hw(x[kt][i] - ms);
-                ps = ps + (float)ph;
+                ts = ts + (float)ph;
                 pb[t][kt >> 1][(kt & 1) * 4 + i] = ph;
             }
-        ps = ps + __shfl_xor(ps, 16);
-        ps = ps + __shfl_xor(ps, 32);
+            ps = ps + tile_sum(ts);
+        }
         s[t].l = s[t].l * corr + ps;
         s[t].m = mn;
 #pragma unroll
@@ -148,18 +170,29 @@ __device__ __forceinline__ void block_step(State<HD> (&s)[NT], const half8 (&qb)
         }
 }
 
-// 8 consecutive elements of a cache row as f16 (f32 caches are rounded to nearest even).
+// 8 consecutive elements of a cache row, loaded now and converted to f16 where they are
+// used (f32 caches round to nearest even), so that a load's wait falls at its use. Lanes
+// with nothing to read load from a zero page instead of branching around the load: a
+// branch would make the compiler wait for every load in flight, prefetches included.
 template <typename KVT>
-__device__ __forceinline__ half8 load8(const KVT* p);
+struct Raw;
 template <>
-__device__ __forceinline__ half8 load8<f16>(const f16* p) {
-    return *(const half8*)p;
-}
+struct Raw<f16> {
+    half8 v;
+    __device__ __forceinline__ void load(const f16* p) { v = *(const half8*)p; }
+    __device__ __forceinline__ half8 get() const { return v; }
+};
 template <>
-__device__ __forceinline__ half8 load8<float>(const float* p) {
-    float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
-    return half8{(f16)a.x, (f16)a.y, (f16)a.z, (f16)a.w, (f16)b.x, (f16)b.y, (f16)b.z, (f16)b.w};
-}
+struct Raw<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = *(const float4*)p;
+        b = *(const float4*)(p + 4);
+    }
+    __device__ __forceinline__ half8 get() const {
+        return half8{(f16)a.x, (f16)a.y, (f16)a.z, (f16)a.w, (f16)b.x, (f16)b.y, (f16)b.z, (f16)b.w};
+    }
+};
 
 __device__ __forceinline__ half8 q_operand(const float* __restrict__ qrow, uint32_t hd0, uint32_t hd, bool ok) {
     if (!ok || hd0 >= hd) return half8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -167,10 +200,10 @@ __device__ __forceinline__ half8 q_operand(const float* __restrict__ qrow, uint3
     return half8{(f16)a.x, (f16)a.y, (f16)a.z, (f16)a.w, (f16)b.x, (f16)b.y, (f16)b.z, (f16)b.w};
 }
 
-// Writes the 8 f16 values of key kl, dims hd0..hd0+7, into the transposed tile vt.
-__device__ __forceinline__ void vt_store(f16* __restrict__ vt, int kl, uint32_t hd0, half8 v) {
+// Writes the 8 f16 values of key kl, dims d0..d0+7, into the transposed tile vt.
+__device__ __forceinline__ void vt_store(f16* __restrict__ vt, int kl, uint32_t d0, half8 v) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) vt[(hd0 + j) * VTS + kl] = v[j];
+    for (int j = 0; j < 8; j++) vt[(d0 + j) * VTS + kl] = v[j];
 }
 
 // Position of the k-th set bit of (lo, hi), k < popcount.
@@ -183,116 +216,305 @@ __device__ __forceinline__ uint32_t nth_set_bit(uint32_t lo, uint32_t hi, uint32
 }
 
 // ---------------------------------------------------------------------------------------
-// Direct kernel: one wave = one row's G heads x one KV head x (one chunk | all chunks).
-template <int HD, typename KVT>
-__global__ __launch_bounds__(64) void attn_direct(const DirectParams p) {
-    __shared__ __attribute__((aligned(16))) f16 vt[HD * VTS];
+// Decode kernel: the G query heads of one row against one KV head for one chunk of the
+// row's list, four waves splitting every block. It writes the chunk's softmax state
+// (m, l, O), or, for a row of one chunk, the normalised output; attn_decode_fold (one-row
+// passes) or attn_combine (multi-row tree passes) combines the chunk states.
+template <int NDT>
+__device__ __forceinline__ void store_state(const State<NDT>& st, float* o_row, float* ml, uint32_t d0, uint32_t hd,
+                                            int g, bool write_ml) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        const uint32_t d = d0 + 16 * dt + 4 * g;
+        if (d < hd) *(float4*)(o_row + d) = float4{st.o[dt][0], st.o[dt][1], st.o[dt][2], st.o[dt][3]};
+    }
+    if (write_ml) *(float2*)ml = float2{st.m, st.l};
+}
+
+template <int HD, typename KVT, bool TREE>
+__global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(const DirectParams p) {
+    constexpr int NDT = HD / 16;                     // output tiles of 16 dims
+    constexpr int DTW = NDT >= 4 ? NDT / 4 : 1;      // output tiles per wave
+    constexpr int DW = 16 * DTW;                     // dims per wave
+    constexpr int LPK = DW / 8;                      // lanes per key in a V load (8 elements each)
+    constexpr int KPI = 64 / LPK;                    // keys per V load
+    constexpr int NVL = BLK / KPI;                   // V loads per block
+    constexpr int NKC = HD / 32;                     // K loads per block (hd chunks)
+    __shared__ __attribute__((aligned(16))) f16 vt[4][DW * VTS];
+    __shared__ float red[2][2][4][16];               // [parity][max, sum][key tile][slot]
+    __shared__ __attribute__((aligned(8))) half4 pt[2][4][4][16];  // [parity][key tile][g][slot]
+    __shared__ __attribute__((aligned(16))) half8 qs[NKC][64];     // Q^T operands by lane
     __shared__ uint32_t tail[64];
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
+    const bool pv = w * DTW < NDT;  // waves with an hd slice (all but for hd <= 32)
+    const uint32_t d0 = 16 * DTW * w;
+    const uint32_t hd = p.hd, kvd = p.nkv * hd;
+    const bool valid = (uint32_t)n < p.G;
+    const KVT* zp = (const KVT*)p.zero;
+
+    // One unit per workgroup, in (item, chunk, KV head) order: the KV heads of one chunk
+    // read one stretch of the cache together. Consecutive workgroups go to the 8 XCDs in
+    // turn, so the KV head turns with the chunk (j + c) to give every XCD a mix of heads:
+    // a fixed head per XCD leaves the XCDs whose head's cache columns map to busier HBM
+    // channels finishing last. The state is stored at the unit's canonical index.
     const uint32_t u = blockIdx.x;
-    const uint32_t per = p.split ? 0u : 1u;
     uint32_t it = 0;
-    for (; it + 1 < p.nitems; it++) {
-        const Item& I = p.items[it];
-        if (u < I.unit0 + p.nkv * (per ? 1u : I.nchunk)) break;
-    }
+    while (it + 1 < p.nitems && u >= p.items[it + 1].unit0) it++;
     const Item I = p.items[it];
-    const uint32_t rem = u - I.unit0;
-    uint32_t kvh, c0, c1;
-    if (p.split) {
-        kvh = rem / I.nchunk;
-        c0 = rem % I.nchunk;
-        c1 = c0 + 1;
-    } else {
-        kvh = rem;
-        c0 = 0;
-        c1 = I.nchunk;
-    }
+    const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = (rem % p.nkv + c) % p.nkv;
+    const size_t cu = (size_t)I.unit0 + (size_t)c * p.nkv + kvh;
+    const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
+    const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
     uint32_t len = I.len;
-    if (p.tree) {
+    if constexpr (TREE) {
         const uint32_t lo = p.masks[2 * I.row], hi = p.masks[2 * I.row + 1];
         const uint32_t ntail = __popc(lo) + __popc(hi);
         len = p.base + ntail;
-        if ((uint32_t)lane < ntail) tail[lane] = p.base + nth_set_bit(lo, hi, lane);
+        if ((uint32_t)tid < ntail) tail[tid] = p.base + nth_set_bit(lo, hi, tid);
         __syncthreads();
     }
-    const uint32_t hd = p.hd, kvd = p.nkv * hd;
-    const bool valid = (uint32_t)n < p.G;
-    const uint32_t h = kvh * p.G + n;
-    half8 qb[1][HD / 32];
-    {
-        const float* qrow = p.q + ((size_t)I.row * p.nh + (valid ? h : 0u)) * hd;
-#pragma unroll
-        for (int c = 0; c < HD / 32; c++) qb[0][c] = q_operand(qrow, 32 * c + 8 * g, hd, valid);
-    }
-    const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
-    const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
+    const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, len);
+
     // Cache slot of list entry k, or ok = false for entries past the list (and for tree
-    // slots past the cache, which a bad mask could name): those read as zeros.
+    // slots past the cache, which a bad mask could name): those read as zeros. A line's
+    // slot is its list entry, with no branch between the loads of a block.
     auto slot_of = [&](uint32_t k, bool& ok) -> uint32_t {
         ok = k < len;
+        if constexpr (!TREE) return ok ? k : 0u;
         if (!ok) return 0u;
-        const uint32_t s = (!p.tree || k < p.base) ? k : tail[k - p.base];
+        const uint32_t s = k < p.base ? k : tail[k - p.base];
         ok = (uint64_t)s + I.kvoff < p.slot_limit;
         return ok ? s : 0u;
     };
-    const uint32_t lens[1] = {len};
-    State<HD> R[1];
-    state_clear(R[0]);
-    constexpr int LPR = HD / 8;       // lanes per V row (16 bytes each)
-    constexpr int KPI = 64 / LPR;     // V rows per load
-    for (uint32_t cc = c0; cc < c1; cc++) {
-        State<HD> cs[1];
-        state_clear(cs[0]);
-        const uint32_t kbeg = cc * I.chunk;
-        const uint32_t kend = min(kbeg + I.chunk, len);
-        for (uint32_t key0 = kbeg; key0 < kend; key0 += BLK) {
-            half8 kreg[4][HD / 32];
+    // K and V of block key0 into registers; entries at or past kb1 read the zero page, so
+    // the prefetch past the last block costs no HBM traffic and needs no branch.
+    auto load_block = [&](uint32_t key0, Raw<KVT> (&kr)[NKC], Raw<KVT> (&vr)[NVL]) {
+        bool ok;
+        const uint32_t kk = key0 + 16 * w + n;
+        const KVT* row = kc + (size_t)slot_of(kk, ok) * kvd;
+        ok = ok && kk < kb1;
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                bool ok;
-                const KVT* row = kc + (size_t)slot_of(key0 + 16 * kt + n, ok) * kvd;
-#pragma unroll
-                for (int c = 0; c < HD / 32; c++) {
-                    uint32_t hd0 = 32 * c + 8 * g;
-                    kreg[kt][c] = (ok && hd0 < hd) ? load8<KVT>(row + hd0) : half8{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < BLK / KPI; i++) {
-                int kl = i * KPI + lane / LPR;
-                uint32_t hd0 = 8 * (lane % LPR);
-                bool ok;
-                const KVT* row = vc + (size_t)slot_of(key0 + kl, ok) * kvd;
-                half8 v = (ok && hd0 < hd) ? load8<KVT>(row + hd0) : half8{0, 0, 0, 0, 0, 0, 0, 0};
-                vt_store(vt, kl, hd0, v);
-            }
-            __syncthreads();
-            block_step<HD, 1>(cs, qb, [&](int kt, int c) { return kreg[kt][c]; }, vt, key0, lens, p.sc);
-            __syncthreads();
+        for (int c2 = 0; c2 < NKC; c2++) {
+            const uint32_t hd0 = 32 * c2 + 8 * g;
+            kr[c2].load((ok && hd0 < hd) ? row + hd0 : zp);
         }
-        if (p.split) {
-            float* po = p.part_o + ((size_t)u * 16 + n) * HD;
+        const uint32_t d = d0 + 8 * (lane % LPK);
 #pragma unroll
-            for (int dt = 0; dt < HD / 16; dt++) {
-                uint32_t d = 16 * dt + 4 * g;
-                if (d < hd) *(float4*)(po + d) = float4{cs[0].o[dt][0], cs[0].o[dt][1], cs[0].o[dt][2], cs[0].o[dt][3]};
-            }
-            if (g == 0) *(float2*)(p.part_ml + ((size_t)u * 16 + n) * 2) = float2{cs[0].m, cs[0].l};
-        } else {
-            fold(R[0], cs[0]);
+        for (int i = 0; i < NVL; i++) {
+            const uint32_t kv = key0 + i * KPI + lane / LPK;
+            const KVT* vrow = vc + (size_t)slot_of(kv, ok) * kvd;
+            vr[i].load((pv && ok && kv < kb1 && d < hd) ? vrow + d : zp);
+        }
+    };
+    // Two register sets in turn: the next block loads into one while the other is used, and
+    // no value is copied between them (a copy would wait for the load).
+    Raw<KVT> kA[NKC], vA[NVL], kB[NKC], vB[NVL];
+    // Q^T operands: wave w loads hd chunks w, w+4, ..., issued ahead of the first block so
+    // that they do not queue behind it; lanes past G or hd read the zero page.
+    constexpr int QPW = (NKC + 3) / 4;
+    float4 qa[QPW], qb[QPW];
+    {
+        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * p.G + (valid ? n : 0)) * hd;
+#pragma unroll
+        for (int j = 0; j < QPW; j++) {
+            const uint32_t c2 = w + 4 * j, hd0 = 32 * c2 + 8 * g;
+            const float* src = (c2 < (uint32_t)NKC && valid && hd0 < hd) ? qrow + hd0 : (const float*)p.zero;
+            qa[j] = *(const float4*)src;
+            qb[j] = *(const float4*)(src + 4);
         }
     }
-    if (!p.split && valid) {
-        float* orow = p.out + ((size_t)I.row * p.nh + h) * hd;
+    load_block(kb0, kA, vA);
 #pragma unroll
-        for (int dt = 0; dt < HD / 16; dt++) {
-            uint32_t d = 16 * dt + 4 * g;
-            if (d < hd)
-                *(float4*)(orow + d) = float4{R[0].o[dt][0] / R[0].l, R[0].o[dt][1] / R[0].l, R[0].o[dt][2] / R[0].l,
-                                              R[0].o[dt][3] / R[0].l};
+    for (int j = 0; j < QPW; j++) {
+        const uint32_t c2 = w + 4 * j;
+        if (c2 < (uint32_t)NKC)
+            qs[c2][lane] = half8{(f16)qa[j].x, (f16)qa[j].y, (f16)qa[j].z, (f16)qa[j].w,
+                                 (f16)qb[j].x, (f16)qb[j].y, (f16)qb[j].z, (f16)qb[j].w};
+    }
+    __syncthreads();
+
+    State<DTW> cs;
+    state_clear(cs);
+    int par = 0;
+    auto compute_block = [&](uint32_t key0, const Raw<KVT> (&kr)[NKC], const Raw<KVT> (&vr)[NVL]) {
+        // Scores of key tile w.
+        f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c2 = 0; c2 < NKC; c2++) st = mfma16(kr[c2].get(), qs[c2][lane], st);
+        float x[4], tm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t k = key0 + 16 * w + 4 * g + i;
+            const float v = st[i] * p.sc;
+            x[i] = (k < len) ? v : -INFINITY;
+            tm = fmaxf(tm, x[i]);
         }
+        tm = tile_max(tm);
+        if (g == 0) red[par][0][w][n] = tm;
+        if (pv) {
+#pragma unroll
+            for (int i = 0; i < NVL; i++) vt_store(vt[w], i * KPI + lane / LPK, 8 * (lane % LPK), vr[i].get());
+        }
+        __syncthreads();
+        const float mx = fmaxf(fmaxf(red[par][0][0][n], red[par][0][1][n]), fmaxf(red[par][0][2][n], red[par][0][3][n]));
+        const float mn = fmaxf(cs.m, mx);
+        const float ms = (mn == -INFINITY) ? 0.0f : mn;
+        const float corr = exp2_hw(cs.m - ms);
+        half4 ph;
+        float ts = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f16 e = (f16)exp2_hw(x[i] - ms);
+            ts = ts + (float)e;
+            ph[i] = e;
+        }
+        ts = tile_sum(ts);
+        if (g == 0) red[par][1][w][n] = ts;
+        pt[par][w][g][n] = ph;
+        __syncthreads();
+        float ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) ps = ps + red[par][1][t][n];
+        cs.l = cs.l * corr + ps;
+        cs.m = mn;
+        if (pv) {
+#pragma unroll
+            for (int dt = 0; dt < DTW; dt++) {
+                f32x4 o = cs.o[dt] * corr;
+#pragma unroll
+                for (int kc2 = 0; kc2 < 2; kc2++) {
+                    const half4 a = pt[par][2 * kc2][g][n], b = pt[par][2 * kc2 + 1][g][n];
+                    const half8 pb = half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                    o = mfma16(v_operand(vt[w], dt, kc2, g, n), pb, o);
+                }
+                cs.o[dt] = o;
+            }
+        }
+        par ^= 1;
+    };
+    if (kb0 < kb1) {
+        for (uint32_t key0 = kb0;;) {
+            load_block(key0 + BLK, kB, vB);
+            compute_block(key0, kA, vA);
+            key0 += BLK;
+            if (key0 >= kb1) break;
+            load_block(key0 + BLK, kA, vA);
+            compute_block(key0, kB, vB);
+            key0 += BLK;
+            if (key0 >= kb1) break;
+        }
+    }
+    if (!valid || !pv) return;
+    if (I.nchunk == 1) {
+        float* orow = p.out + ((size_t)I.row * p.nh + kvh * p.G + n) * hd;
+#pragma unroll
+        for (int dt = 0; dt < DTW; dt++) {
+            const uint32_t d = d0 + 16 * dt + 4 * g;
+            if (d < hd)
+                *(float4*)(orow + d) =
+                    float4{cs.o[dt][0] / cs.l, cs.o[dt][1] / cs.l, cs.o[dt][2] / cs.l, cs.o[dt][3] / cs.l};
+        }
+    } else {
+        store_state(cs, p.part_o + (cu * 16 + n) * HD, p.part_ml + (cu * 16 + n) * 2, d0, hd, g,
+                    w == 0 && g == 0);
+    }
+}
+
+// The combination of a one-row list's chunk states, for one (item, KV head, slot): with
+// M = the largest chunk max (exact in any order) and w_c = 2^(m_c - M), O = sum_c w_c o_c
+// and L = sum_c w_c l_c, each summed by a perfect binary tree over the chunk index padded
+// to a power of two with zeros (a zero adds exactly, so the padding width does not change
+// the sums), and out = O / L. The tree is fixed by the chunk count alone.
+// A workgroup takes FOLD_DIMS dims of one slot: thread (cl, dg) holds the aligned run of R
+// chunks cl*R .. cl*R+R-1 (32 runs) for dims 4dg .. 4dg+3, sums it as a subtree in
+// registers, then the runs pair up across lanes (cl^1, cl^2, cl^4: lane bits 3-5) and
+// across the four waves in LDS. Every load is issued before the first use.
+constexpr int FOLD_DIMS = 32;
+constexpr int FOLD_RUNS = 32;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_fold(const DirectParams p) {
+    __shared__ float wmax[4];
+    __shared__ float4 wo[4][8];
+    __shared__ float wl[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t dg = tid & 7, cl = tid >> 3;
+    const uint32_t hd = p.hd, nslice = (hd + FOLD_DIMS - 1) / FOLD_DIMS;
+    // Workgroup -> (item, KV head, slot, dim slice) over the items with more than one chunk.
+    uint32_t b = blockIdx.x, it = 0;
+    for (;; it++) {
+        const uint32_t here = p.items[it].nchunk > 1 ? p.nkv * p.G * nslice : 0u;
+        if (b < here || it + 1 >= p.nitems) break;
+        b -= here;
+    }
+    const Item I = p.items[it];
+    const uint32_t slice = b % nslice, kvh = (b / nslice) / p.G, slot = (b / nslice) % p.G;
+    const uint32_t nch = I.nchunk, d = slice * FOLD_DIMS + 4 * dg;
+    const bool dok = d < hd;
+    uint32_t N = FOLD_RUNS;
+    while (N < nch) N <<= 1;
+    const uint32_t R = N / FOLD_RUNS;
+    // Leaves of this thread's run, loaded together; chunks past nch are zero leaves.
+    constexpr int RMAX = 8;
+    float2 ml[RMAX];
+    float4 o[RMAX];
+#pragma unroll
+    for (int j = 0; j < RMAX; j++) {
+        const uint32_t c = cl * R + j;
+        const bool live = (uint32_t)j < R && c < nch;
+        const size_t at = ((size_t)I.unit0 + (size_t)(live ? c : 0u) * p.nkv + kvh) * 16 + slot;
+        ml[j] = live ? *(const float2*)(p.part_ml + at * 2) : float2{-INFINITY, 0.0f};
+        o[j] = (live && dok) ? *(const float4*)(p.part_o + at * HD + d) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < RMAX; j++) mx = fmaxf(mx, ml[j].x);
+    mx = fmaxf(mx, __shfl_xor(mx, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (lane == 0) wmax[w] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    // Leaf values, then the run's subtree (R is a power of two <= RMAX; unused leaves are 0
+    // and sit past the run, so the pairing below is the subtree's).
+    float4 vo[RMAX];
+    float vl[RMAX];
+#pragma unroll
+    for (int j = 0; j < RMAX; j++) {
+        const float wc = exp2_hw(ml[j].x - Ms);
+        vo[j] = float4{o[j].x * wc, o[j].y * wc, o[j].z * wc, o[j].w * wc};
+        vl[j] = ml[j].y * wc;
+    }
+#pragma unroll
+    for (int width = RMAX; width > 1; width >>= 1)
+#pragma unroll
+        for (int j = 0; j < width / 2; j++) {
+            if ((uint32_t)width <= R) {
+                vo[j] = float4{vo[2 * j].x + vo[2 * j + 1].x, vo[2 * j].y + vo[2 * j + 1].y,
+                               vo[2 * j].z + vo[2 * j + 1].z, vo[2 * j].w + vo[2 * j + 1].w};
+                vl[j] = vl[2 * j] + vl[2 * j + 1];
+            }
+        }
+    float4 so = vo[0];
+    float sl = vl[0];
+#pragma unroll
+    for (int x = 8; x <= 32; x <<= 1) {
+        so = float4{so.x + __shfl_xor(so.x, x), so.y + __shfl_xor(so.y, x), so.z + __shfl_xor(so.z, x),
+                    so.w + __shfl_xor(so.w, x)};
+        sl = sl + __shfl_xor(sl, x);
+    }
+    if (lane < 8) wo[w][lane] = so;
+    if (lane == 0) wl[w] = sl;
+    __syncthreads();
+    if (tid < 8 && dok) {
+        const float4 a = wo[0][tid], b2 = wo[1][tid], c = wo[2][tid], e = wo[3][tid];
+        const float L = (wl[0] + wl[1]) + (wl[2] + wl[3]);
+        const float4 O = float4{(a.x + b2.x) + (c.x + e.x), (a.y + b2.y) + (c.y + e.y), (a.z + b2.z) + (c.z + e.z),
+                                (a.w + b2.w) + (c.w + e.w)};
+        *(float4*)(p.out + ((size_t)I.row * p.nh + kvh * p.G + slot) * hd + d) =
+            float4{O.x / L, O.y / L, O.z / L, O.w / L};
     }
 }
 
@@ -313,13 +535,11 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
     // Heaviest row blocks (latest rows, longest lists) first, across KV heads.
-    const uint32_t ngrp = p.nkv * p.nrb;
     const uint32_t gi_launch = p.split ? blockIdx.x / p.nchunk : blockIdx.x;
     const uint32_t cs_idx = p.split ? blockIdx.x % p.nchunk : 0u;
     const uint32_t kvh = gi_launch % p.nkv;
     const uint32_t rbi = p.nrb - 1u - gi_launch / p.nkv;
     const uint32_t grp = kvh * p.nrb + rbi;  // canonical group of the partials
-    (void)ngrp;
     const uint32_t r0 = rbi * p.rb;
     const uint32_t rlast = min(r0 + p.rb, p.rows) - 1u;
     const uint32_t maxlen = p.pos + rlast + 1u;
@@ -353,7 +573,8 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
         kb1 = maxlen;
     }
 
-    half8 kpre[LOADS], vpre[LOADS];
+    const KVT* zp = (const KVT*)p.zero;
+    Raw<KVT> kpre[LOADS], vpre[LOADS];
     auto load_block = [&](uint32_t key0) {
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
@@ -361,9 +582,9 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
             int kr = e / LPR;
             uint32_t hd0 = 8 * (e % LPR);
             uint32_t k = key0 + kr;
-            bool ok = k < maxlen && hd0 < hd;
-            kpre[i] = ok ? load8<KVT>(kcb + (size_t)k * kvd + hd0) : half8{0, 0, 0, 0, 0, 0, 0, 0};
-            vpre[i] = ok ? load8<KVT>(vcb + (size_t)k * kvd + hd0) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+            bool ok = k < kb1 && hd0 < hd;
+            kpre[i].load(ok ? kcb + (size_t)k * kvd + hd0 : zp);
+            vpre[i].load(ok ? vcb + (size_t)k * kvd + hd0 : zp);
         }
     };
     auto store_block = [&](int stage) {
@@ -372,12 +593,12 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
             int e = i * NTH + tid;
             int kr = e / LPR;
             uint32_t hd0 = 8 * (e % LPR);
-            *(half8*)&kl[stage][kr * KS + hd0] = kpre[i];
-            vt_store(vt[stage], kr, hd0, vpre[i]);
+            *(half8*)&kl[stage][kr * KS + hd0] = kpre[i].get();
+            vt_store(vt[stage], kr, hd0, vpre[i].get());
         }
     };
 
-    State<HD> R[NT], cs[NT];
+    State<HD / 16> R[NT], cs[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         state_clear(R[t]);
@@ -397,14 +618,14 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
                 state_clear(cs[t]);
             }
         }
-        const bool more = key0 + BLK < kb1;
-        if (more) load_block(key0 + BLK);
+        // The next block (zeros past this workgroup's range: no branch, no HBM traffic).
+        load_block(key0 + BLK);
         const f16* kls = kl[stage];
         block_step<HD, NT>(
             cs, qb,
             [&](int kt, int c) { return *(const half8*)&kls[(16 * kt + n) * KS + 32 * c + 8 * g]; },
             vt[stage], key0, len, p.sc);
-        if (more) store_block(stage ^ 1);
+        store_block(stage ^ 1);
         __syncthreads();
         stage ^= 1;
     }
@@ -439,52 +660,120 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// The left fold of split chunks, in chunk order, then O / L. One workgroup per group:
-// direct launches: (item, KV head); shared launches: (KV head, row block).
+// The left fold of split chunks, in chunk order, then O / L: one wave per (output slot,
+// slice of 64 dims). Chunk c's fold weights are a_c = 2^(M_{c-1} - M_c) and
+// b_c = 2^(m_c - M_c), with M_c the running maximum, exactly as fold() computes them; the
+// running maxima are a prefix max, so all weights are computed at once and only
+// O = O*a_c + o_c*b_c (and the same for L) runs chunk by chunk, from partials staged in LDS
+// by loads that are all in flight together.
+constexpr int CMB_PASS = 1024;  // chunks whose weights are computed at once
+constexpr int CMB_STAGE = 128;  // chunks of partial values staged at once
+constexpr int CMB_BATCH = 8;    // recurrence steps whose operands are read ahead
+
 template <int HD>
-__global__ __launch_bounds__(256) void attn_combine(const CombineParams p) {
-    const uint32_t grp = blockIdx.x;
+__global__ __launch_bounds__(64) void attn_combine(const CombineParams p) {
+    __shared__ float sm[CMB_PASS], sx[CMB_PASS], sa[CMB_PASS], sb[CMB_PASS], sl[CMB_PASS];
+    __shared__ __attribute__((aligned(16))) float so[CMB_STAGE * 64];
+    const int lane = threadIdx.x;
     const uint32_t hd = p.hd;
-    uint32_t unit0, nchunk, nslot, kvh;
-    uint32_t item = 0, rbi = 0;
+    const uint32_t nslice = (hd + 63) / 64;
+    const uint32_t slice = blockIdx.x % nslice, rest = blockIdx.x / nslice;
+    const uint32_t grp = rest / p.slots_out, slot = rest % p.slots_out;
+    uint32_t unit0, nchunk, r, h, step;  // chunk c's state is unit unit0 + c * step
     if (p.shared) {
-        kvh = grp / p.nrb;
-        rbi = grp % p.nrb;
+        const uint32_t kvh = grp / p.nrb, rbi = grp % p.nrb;
+        const uint32_t gh = slot / p.rb, rl = slot % p.rb;
+        r = rbi * p.rb + rl;
+        if (gh >= p.G || r >= p.rows) return;
+        h = kvh * p.G + gh;
         unit0 = grp * p.nchunk;
         nchunk = p.nchunk;
-        nslot = p.slots;
-    } else {
-        item = grp / p.nkv;
-        kvh = grp % p.nkv;
-        unit0 = p.items[item].unit0 + kvh * p.items[item].nchunk;
+        step = 1;
+    } else {  // decode kernel states, in (item, chunk, KV head) order
+        const uint32_t item = grp / p.nkv, kvh = grp % p.nkv;
+        r = p.items[item].row;
+        h = kvh * p.G + slot;
+        unit0 = p.items[item].unit0 + kvh;
         nchunk = p.items[item].nchunk;
-        nslot = p.G;
+        step = p.nkv;
+        if (nchunk == 1) return;  // the decode kernel wrote this row's output itself
     }
-    for (uint32_t e = threadIdx.x; e < nslot * hd; e += blockDim.x) {
-        uint32_t sl = e / hd, d = e % hd;
-        uint32_t r, h;
-        if (p.shared) {
-            uint32_t gh = sl / p.rb, rl = sl % p.rb;
-            r = rbi * p.rb + rl;
-            if (gh >= p.G || rl >= p.rb || r >= p.rows) continue;
-            h = kvh * p.G + gh;
-        } else {
-            r = p.items[item].row;
-            h = kvh * p.G + sl;
+    const uint32_t stride = p.slots;  // partial slots per unit
+    const uint32_t dbase = 64 * slice;
+    const uint32_t d = dbase + lane;
+    float Mrun = -INFINITY, L = 0.0f, O = 0.0f;
+    for (uint32_t cb = 0; cb < nchunk; cb += CMB_PASS) {
+        const uint32_t cnt = min((uint32_t)CMB_PASS, nchunk - cb);
+        for (uint32_t c = lane; c < cnt; c += 64) {
+            const float2 ml = *(const float2*)(p.part_ml + ((size_t)unit0 + (size_t)(cb + c) * step) * stride * 2 + slot * 2);
+            sm[c] = ml.x;
+            sl[c] = ml.y;
         }
-        float M = -INFINITY, L = 0.0f, O = 0.0f;
-        for (uint32_t c = 0; c < nchunk; c++) {
-            size_t at = (size_t)(unit0 + c) * p.slots + sl;
-            float2 ml = *(const float2*)(p.part_ml + at * 2);
-            float o = p.part_o[at * HD + d];
+        __syncthreads();
+        // Inclusive prefix max over the pass: each lane a segment, then across lanes.
+        const uint32_t seg = (cnt + 63) / 64, s0 = lane * seg, s1 = min(s0 + seg, cnt);
+        float run = -INFINITY;
+        for (uint32_t c = s0; c < s1; c++) {
+            run = fmaxf(run, sm[c]);
+            sx[c] = run;
+        }
+        float incl = run;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float t = __shfl_up(incl, off);
+            if (lane >= off) incl = fmaxf(incl, t);
+        }
+        float excl = __shfl_up(incl, 1);
+        if (lane == 0) excl = -INFINITY;
+        for (uint32_t c = s0; c < s1; c++) sx[c] = fmaxf(excl, sx[c]);
+        __syncthreads();
+        for (uint32_t c = lane; c < cnt; c += 64) {
+            const float Mprev = c == 0 ? Mrun : fmaxf(Mrun, sx[c - 1]);
             float a, b, mn;
-            merge_coef(M, ml.x, a, b, mn);
-            L = L * a + ml.y * b;
-            O = O * a + o * b;
-            M = mn;
+            merge_coef(Mprev, sm[c], a, b, mn);
+            sa[c] = a;
+            sb[c] = b;
         }
-        p.out[((size_t)r * p.nh + h) * hd + d] = O / L;
+        __syncthreads();
+        for (uint32_t st0 = 0; st0 < cnt; st0 += CMB_STAGE) {
+            const uint32_t k = min((uint32_t)CMB_STAGE, cnt - st0);
+            // 16 float4 per chunk slice: k * 16 loads over 64 lanes, issued before any store.
+            float4 v[CMB_STAGE * 16 / 64];
+#pragma unroll
+            for (int i = 0; i < CMB_STAGE * 16 / 64; i++) {
+                const uint32_t e = i * 64 + lane, cc = e / 16, q = 4 * (e % 16);
+                const float* src = (cc < k && dbase + q < hd)
+                                       ? p.part_o + (((size_t)unit0 + (size_t)(cb + st0 + cc) * step) * stride + slot) * HD + dbase + q
+                                       : (const float*)p.zero;
+                v[i] = *(const float4*)src;
+            }
+#pragma unroll
+            for (int i = 0; i < CMB_STAGE * 16 / 64; i++) *(float4*)&so[(i * 64 + lane) * 4] = v[i];
+            __syncthreads();
+            for (uint32_t c0 = 0; c0 < k; c0 += CMB_BATCH) {
+                float ba[CMB_BATCH], bb[CMB_BATCH], bl[CMB_BATCH], bo[CMB_BATCH];
+#pragma unroll
+                for (int j = 0; j < CMB_BATCH; j++) {
+                    const uint32_t c = min(c0 + j, k - 1);
+                    ba[j] = sa[st0 + c];
+                    bb[j] = sb[st0 + c];
+                    bl[j] = sl[st0 + c];
+                    bo[j] = so[c * 64 + lane];
+                }
+#pragma unroll
+                for (int j = 0; j < CMB_BATCH; j++) {
+                    if (c0 + j < k) {
+                        L = L * ba[j] + bl[j] * bb[j];
+                        O = O * ba[j] + bo[j] * bb[j];
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        Mrun = fmaxf(Mrun, sx[cnt - 1]);
+        __syncthreads();
     }
+    if (d < hd) p.out[((size_t)r * p.nh + h) * hd + d] = O / L;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -492,24 +781,24 @@ __global__ __launch_bounds__(256) void attn_combine(const CombineParams p) {
 
 static uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
-// Chunk of a one-row call: about 128 chunks of the list, 64..256 entries, so a decode step
-// fills the CUs from a few thousand visible slots up; from 16385 on it is CHUNK_MULTI.
-uint32_t decode_chunk(uint64_t len) {
-    uint64_t want = (len + 127) / 128;
-    uint32_t c = 64;
-    while (c < want && c < CHUNK_MULTI) c <<= 1;
+// Chunk of a one-row call with nkv KV heads: the smallest power of two of at least one block
+// that cuts the list into at most 512 / nkv chunks (at least 1, at most 256, what
+// attn_decode_fold takes): about two units of several blocks per CU, so that the grid is
+// resident at once and every CU streams to the end without a second dispatch round.
+// Any u32 list length fits (2^24 * 256 = 2^32).
+uint32_t decode_chunk(uint64_t len, uint32_t nkv) {
+    uint64_t most = 512 / (nkv ? nkv : 1);
+    if (most < 1) most = 1;
+    if (most > 8 * FOLD_RUNS) most = 8 * FOLD_RUNS;
+    uint32_t c = BLK;
+    while ((len + c - 1) / c > most && c < (1u << 24)) c <<= 1;
     return c;
-}
-
-template <int HD, typename KVT>
-static hipError_t launch_direct_t(DirectParams& dp, uint32_t units, hipStream_t s) {
-    hipLaunchKernelGGL((attn_direct<HD, KVT>), dim3(units), dim3(64), 0, s, dp);
-    return hipGetLastError();
 }
 
 template <int HD>
 static hipError_t launch_combine_t(const CombineParams& cp, uint32_t groups, hipStream_t s) {
-    hipLaunchKernelGGL((attn_combine<HD>), dim3(groups), dim3(256), 0, s, cp);
+    const uint32_t nslice = (cp.hd + 63) / 64;
+    hipLaunchKernelGGL((attn_combine<HD>), dim3(groups * cp.slots_out * nslice), dim3(64), 0, s, cp);
     return hipGetLastError();
 }
 
@@ -526,73 +815,95 @@ static int pad_hd(uint32_t hd) {
     return 256;
 }
 
-#define BCHIP_DISPATCH_HD(hdp, CALL)            \
-    switch (hdp) {                              \
+#define BCHIP_DISPATCH_HD(hdp, CALL)                       \
+    switch (hdp) {                                         \
         case 32: { constexpr int HD = 32; CALL; } break;   \
         case 64: { constexpr int HD = 64; CALL; } break;   \
         case 128: { constexpr int HD = 128; CALL; } break; \
         default: { constexpr int HD = 256; CALL; } break;  \
     }
 
-hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
-                            Workspace& ws, hipStream_t s) {
+template <int HD>
+static hipError_t launch_combine_t(const CombineParams& cp, uint32_t groups, hipStream_t s);
+
+template <int HD, typename KVT>
+static hipError_t launch_decode_t(DirectParams& dp, uint32_t folds, const CombineParams* left, hipStream_t s) {
+    const dim3 block(256);
+    const dim3 grid(dp.nunits);
+    if (dp.tree)
+        hipLaunchKernelGGL((attn_decode<HD, KVT, true>), grid, block, 0, s, dp);
+    else
+        hipLaunchKernelGGL((attn_decode<HD, KVT, false>), grid, block, 0, s, dp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || folds == 0) return e;
+    if (left) return launch_combine_t<HD>(*left, dp.nitems * dp.nkv, s);
+    hipLaunchKernelGGL((attn_decode_fold<HD>), dim3(folds), block, 0, s, dp);
+    return hipGetLastError();
+}
+
+hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s) {
     DirectParams dp{};
+    dp.zero = ws.zero;
     dp.q = a.q;
     dp.kc = a.kc;
     dp.vc = a.vc;
     dp.out = a.out;
+    dp.masks = a.masks;
+    dp.slot_limit = a.slot_limit;
     dp.nh = a.nh;
     dp.nkv = a.nkv;
     dp.hd = a.hd;
     dp.G = a.nh / a.nkv;
-    dp.masks = a.masks;
-    dp.slot_limit = a.slot_limit;
     dp.base = a.pos;
     dp.tree = a.tree;
     dp.sc = a.scale * LOG2E;
     dp.nitems = nitems;
-    uint64_t total_chunks = 0;
-    for (uint32_t i = 0; i < nitems; i++) total_chunks += items[i].nchunk;
-    // Split by chunk unless the launch already has plenty of waves.
-    dp.split = (total_chunks > nitems) && (uint64_t)nitems * a.nkv < 1024;
-    uint32_t units = 0;
+    uint32_t units = 0, folds = 0;
+    const uint32_t nslice = (a.hd + FOLD_DIMS - 1) / FOLD_DIMS;
     for (uint32_t i = 0; i < nitems; i++) {
-        dp.items[i] = items[i];
-        dp.items[i].unit0 = units;
-        units += a.nkv * (dp.split ? items[i].nchunk : 1u);
+        Item& I = dp.items[i];
+        I = items[i];
+        I.unit0 = units;
+        units += a.nkv * I.nchunk;
+        if (I.nchunk > 1) folds += a.nkv * dp.G * nslice;
+        if (a.rows == 1 && I.nchunk > 8 * FOLD_RUNS) return hipErrorInvalidValue;  // decode_chunk keeps to 256
     }
+    dp.nunits = units;
     const int hdp = pad_hd(a.hd);
-    if (dp.split) {
-        hipError_t e = ws.reserve((size_t)units * 16, (size_t)hdp);
-        if (e != hipSuccess) return e;
-        dp.part_o = ws.o;
-        dp.part_ml = ws.ml;
-    }
-    hipError_t e;
-    if (a.kv_type == 1) {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_direct_t<HD, f16>(dp, units, s)));
-    } else {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_direct_t<HD, float>(dp, units, s)));
-    }
-    if (e != hipSuccess || !dp.split) return e;
+    hipError_t e = ws.reserve((size_t)units * 16, (size_t)hdp);
+    if (e != hipSuccess) return e;
+    dp.part_o = ws.o;
+    dp.part_ml = ws.ml;
+    // Multi-row tree passes fold chunks left to right, as every multi-row line does, so that
+    // a tree row matches its line bit for bit; one-row passes use the tree combination.
     CombineParams cp{};
-    cp.out = a.out;
-    cp.part_o = ws.o;
-    cp.part_ml = ws.ml;
-    cp.nh = a.nh;
-    cp.nkv = a.nkv;
-    cp.hd = a.hd;
-    cp.G = dp.G;
-    cp.slots = 16;
-    cp.shared = 0;
-    cp.nitems = nitems;
-    for (uint32_t i = 0; i < nitems; i++) cp.items[i] = dp.items[i];
-    BCHIP_DISPATCH_HD(hdp, e = (launch_combine_t<HD>(cp, nitems * a.nkv, s)));
+    const bool left = a.rows >= 2;
+    if (left) {
+        cp.zero = ws.zero;
+        cp.out = a.out;
+        cp.part_o = ws.o;
+        cp.part_ml = ws.ml;
+        cp.nh = a.nh;
+        cp.nkv = a.nkv;
+        cp.hd = a.hd;
+        cp.G = dp.G;
+        cp.slots = 16;
+        cp.slots_out = dp.G;
+        cp.shared = 0;
+        cp.nitems = nitems;
+        for (uint32_t i = 0; i < nitems; i++) cp.items[i] = dp.items[i];
+    }
+    if (a.kv_type == 1) {
+        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, f16>(dp, folds, left ? &cp : nullptr, s)));
+    } else {
+        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, float>(dp, folds, left ? &cp : nullptr, s)));
+    }
     return e;
 }
 
 hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     SharedParams sp{};
+    sp.zero = ws.zero;
     sp.q = a.q;
     sp.kc = a.kc;
     sp.vc = a.vc;
@@ -638,6 +949,7 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     }
     if (e != hipSuccess || !sp.split) return e;
     CombineParams cp{};
+    cp.zero = ws.zero;
     cp.out = a.out;
     cp.part_o = ws.o;
     cp.part_ml = ws.ml;
@@ -646,6 +958,7 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     cp.hd = a.hd;
     cp.G = sp.G;
     cp.slots = SL;
+    cp.slots_out = SL;
     cp.shared = 1;
     cp.rows = a.rows;
     cp.rb = sp.rb;

@@ -116,19 +116,24 @@ namespace bchip {
 
 hipError_t Workspace::reserve(size_t need_slots, size_t hd_pad) {
     if (need_slots <= slots && hd_pad <= hdp && o) return hipSuccess;
-    size_t ns = std::max(need_slots, slots), nh = std::max(hd_pad, hdp);
-    release();
-    hipError_t e = hipMalloc((void**)&o, ns * nh * sizeof(float));
+    const size_t ns = std::max(need_slots, slots), nh = std::max(hd_pad, hdp);
+    if (o) (void)hipFree(o);
+    if (ml) (void)hipFree(ml);
+    o = ml = nullptr;
+    slots = 0;
+    hdp = nh;
+    hipError_t e = hipMalloc((void**)&o, ns * hdp * sizeof(float));
     if (e != hipSuccess) return e;
     e = hipMalloc((void**)&ml, ns * 2 * sizeof(float));
-    if (e != hipSuccess) {
-        (void)hipFree(o);
-        o = nullptr;
-        return e;
-    }
+    if (e != hipSuccess) return e;
     slots = ns;
-    hdp = nh;
     return hipSuccess;
+}
+
+hipError_t Workspace::init() {
+    hipError_t e = hipMalloc(&zero, ZERO_BYTES);
+    if (e != hipSuccess) return e;
+    return hipMemset(zero, 0, ZERO_BYTES);
 }
 
 void Workspace::release() {
@@ -163,6 +168,7 @@ int bchip_init(int device, bchip_ctx** out) {
     c->device = device;
     c->name = prop.name;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = c->ws.init();
     if (e == hipSuccess) e = hipEventCreate(&c->t0);
     if (e == hipSuccess) e = hipEventCreate(&c->t1);
     if (e != hipSuccess) {
@@ -178,6 +184,7 @@ int bchip_destroy(bchip_ctx* c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     c->ws.release();
+    if (c->ws.zero) (void)hipFree(c->ws.zero);
     for (auto& a : c->allocs) (void)hipFree((void*)a.first);
     if (c->t0) (void)hipEventDestroy(c->t0);
     if (c->t1) (void)hipEventDestroy(c->t1);
@@ -373,11 +380,16 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     AttnCall a{q, kc, vc, kv_type, out, masks, tree ? 1u : 0u, rows, nh, nkv, hd, pos, scale, limit};
     hipError_t e;
     if (rows == 1 || tree) {
-        const uint32_t chunk = rows == 1 ? decode_chunk(slots) : CHUNK_MULTI;
+        const uint32_t chunk = rows == 1 ? decode_chunk(slots, nkv) : CHUNK_MULTI;
         Item items[MAX_ITEMS];
         for (uint32_t r = 0; r < rows; r++) {
             const uint64_t upto = tree ? slots : (uint64_t)pos + r + 1;
-            items[r] = Item{r, (uint32_t)upto, 0u, (uint32_t)((upto + chunk - 1) / chunk), chunk, 0ull};
+            Item& I = items[r];
+            I = Item{};
+            I.row = r;
+            I.len = (uint32_t)upto;
+            I.nchunk = (uint32_t)((upto + chunk - 1) / chunk);
+            I.chunk = chunk;
         }
         e = direct_attention(a, items, rows, c->ws, c->stream);
     } else {
@@ -414,8 +426,14 @@ int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const v
         Item items[MAX_ITEMS];
         for (uint32_t i = 0; i < ns; i++) {
             const uint32_t len = seq_lens[s0 + i];
-            const uint32_t chunk = decode_chunk(len);
-            items[i] = Item{s0 + i, len, 0u, (len + chunk - 1) / chunk, chunk, kv_offsets[s0 + i]};
+            const uint32_t chunk = decode_chunk(len, nkv);
+            Item& I = items[i];
+            I = Item{};
+            I.row = s0 + i;
+            I.len = len;
+            I.nchunk = (len + chunk - 1) / chunk;
+            I.chunk = chunk;
+            I.kvoff = kv_offsets[s0 + i];
         }
         HIP_TRY(direct_attention(a, items, ns, c->ws, c->stream), "ragged attention");
     }

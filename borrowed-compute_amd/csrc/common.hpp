@@ -33,37 +33,41 @@ __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// A row of work for the direct (one wave, one 16-slot tile) attention kernel: the G query
-// heads of one row against one KV head.
+// A row of work for the decode kernel: the G query heads of one row against each KV head.
+// Its list is cut into nchunk chunks of `chunk` entries, one unit of work each per KV head.
 struct Item {
     uint32_t row;    // row of q / out
     uint32_t len;    // visible list length (tree rows: computed from the mask)
     uint32_t unit0;  // first unit of this item in the launch
     uint32_t nchunk; // chunks of this row's list (an upper bound for tree rows)
     uint32_t chunk;  // list entries per chunk (multiple of BLK)
+    uint32_t pad_;
     uint64_t kvoff;  // slot offset of the row's cache (ragged pools), else 0
 };
 
+// zero: a device page of zeros that lanes with nothing to read load from.
 struct DirectParams {
+    const void* zero;
     const float* q;
     const void* kc;
     const void* vc;
     float* out;
-    float* part_o;  // [unit][16][HD]
+    float* part_o;  // [unit][16][HD]: chunk states
     float* part_ml; // [unit][16][2]
+    uint32_t nunits;
     const uint32_t* masks; // tree: two words per row
     uint32_t nh, nkv, hd, G;
     uint32_t base;  // tree: first tree slot
     uint32_t tree;
     uint64_t slot_limit; // slots the caches hold (tree slots past it read as absent)
     float sc;       // scale * log2(e)
-    uint32_t split; // 1: a unit is one chunk of one item, written as a partial
     uint32_t nitems;
     Item items[MAX_ITEMS];
 };
 
 // Multi-row line attention: a workgroup takes rb rows x all G heads of one KV head.
 struct SharedParams {
+    const void* zero;
     const float* q;
     const void* kc;
     const void* vc;
@@ -80,14 +84,16 @@ struct SharedParams {
 };
 
 struct CombineParams {
+    const void* zero;
     float* out;
     const float* part_o;
     const float* part_ml;
     uint32_t nh, nkv, hd, G;
-    uint32_t slots;   // partial slots per unit (16 for direct, SL for shared)
-    // direct: one group per (item, kvh); shared: one group per (kvh, row block)
+    uint32_t slots;     // partial slots per unit (16 for decode launches, SL for shared)
+    uint32_t slots_out; // workgroups per group: one per output slot
+    // decode launches: one group per (item, KV head); shared: one per (KV head, row block)
     uint32_t shared;
-    uint32_t rows, rb, nrb, nchunk; // shared
+    uint32_t rows, rb, nrb, nchunk; // shared launches
     uint32_t nitems;
     Item items[MAX_ITEMS];
 };

@@ -11,12 +11,16 @@ namespace bchip {
 
 // Device scratch for split-K partials, owned by a context and grown on demand.
 struct Workspace {
-    float* o = nullptr;   // [units*slots][hd_pad]
-    float* ml = nullptr;  // [units*slots][2]
+    float* o = nullptr;    // [units*slots][hd_pad]: chunk states
+    float* ml = nullptr;   // [units*slots][2]
+    void* zero = nullptr;  // ZERO_BYTES of zeros
     size_t slots = 0, hdp = 0;
+    hipError_t init();     // allocates the zero page
     hipError_t reserve(size_t need_slots, size_t hd_pad);
     void release();
 };
+
+constexpr size_t ZERO_BYTES = 4096;
 
 struct AttnCall {
     const float* q;
@@ -30,7 +34,7 @@ struct AttnCall {
     uint64_t slot_limit;  // slots both caches hold (all slots a call may read when unknown)
 };
 
-uint32_t decode_chunk(uint64_t len);
+uint32_t decode_chunk(uint64_t len, uint32_t nkv);
 hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
                             Workspace& ws, hipStream_t s);
 hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s);

@@ -121,8 +121,9 @@ int bchip_rope_append(bchip_ctx* ctx, float* q, const float* k, const float* v, 
  * Every row of a multi-row call (rows >= 2) is computed by the same fixed-order
  * arithmetic, which depends only on the row's q and its visible slot list: results are
  * identical whatever the batch, the row's index, or whether it is a tree node or a line
- * token. A one-row call computes in the same order, with chunks sized by its length
- * (identical to a batch row from 16384 visible slots up, otherwise within rounding). */
+ * token. A one-row call (a decode step) splits its list across the GPU and folds the
+ * pieces in a fixed two-level order set by its length alone: deterministic, and within
+ * rounding of the same row in a batch (the reference allows 1e-4, model.rs:641-642). */
 int bchip_attention(bchip_ctx* ctx, const float* q, const void* kc, const void* vc,
                     uint32_t kv_type, float* out, const uint32_t* masks, uint32_t tree,
                     uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t pos,
@@ -133,7 +134,8 @@ int bchip_attention(bchip_ctx* ctx, const float* q, const void* kc, const void* 
  * q[i] [nh][hd] sees the seq_lens[i] slots kv_offsets[i] .. kv_offsets[i]+seq_lens[i]-1 of
  * the shared kc/vc pool (a ragged layout). Each sequence's result equals bchip_attention
  * with rows = 1, pos = seq_lens[i]-1 on its own slots, bit for bit. seq_lens and
- * kv_offsets are host arrays; nseq <= 256. */
+ * kv_offsets are host arrays; nseq <= 256. Not for graph capture across calls with
+ * different lengths: the plan is made on the host from seq_lens. */
 int bchip_attention_ragged(bchip_ctx* ctx, const float* q, const void* kc, const void* vc,
                            uint32_t kv_type, float* out, const uint32_t* seq_lens,
                            const uint64_t* kv_offsets, uint32_t nseq, uint32_t nh,
