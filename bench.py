@@ -9,9 +9,11 @@ the 256 MB MALL: labelled so), causal prefill at 2048 and 8192 tokens (TFLOP/s, 
 the Llama-3-70B stage share's verify steps, Qwen2.5-7B ragged batched decode
 (configs[3]).
 
-roofline: the decode attention kernel's algorithmic bytes per launch (2 * L * n_kv * hd * 2
-bytes of f16 K and V, each read once) over its mean launch time, from HIP events recorded
-around every attention launch of the timed region on the library's stream.
+roofline: the decode attention call's algorithmic bytes per launch (2 * L * n_kv * hd * 2
+bytes of f16 K and V, each read once) over its mean duration, from HIP events recorded
+around every attention call of the timed region on the library's stream (the call is the
+attn_decode kernel plus the small attn_decode_fold; the events include the gap between
+them). traffic: measured HBM bytes per call from the committed rocprofv3 counter summary.
 
 cpu_baseline: bc-infer's CPU attention as the oracle's C restatement (single thread, as
 the reference runs it: crates/bc-infer/src/model.rs:391-403, 448-481), timed on this
@@ -299,6 +301,20 @@ def cpu_baseline(layers=5, ctx_len=32768, nh=32, nkv=8, hd=128):
             "cpu": _cpu_model(), "nproc": os.cpu_count()}
 
 
+def profiled_traffic(ctx_len):
+    """HBM bytes per decode attention call (decode + fold kernels) from the committed counter
+    summary: FETCH_SIZE and WRITE_SIZE passes of rocprofv3 over this script, scaled by the
+    same counters' reading for a copy of known size. None when the summary is absent or was
+    taken at another context length."""
+    path = os.path.join(ROOT, "profiles", "attn_decode_llama8b_32k.txt")
+    if ctx_len != 32768 or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -384,7 +400,9 @@ def main():
                                f"f16 KV at {args.ctx} slots, RoPE theta 5e5 fused with the K/V append, 32 layers",
                    "ctx": args.ctx, "layers": 32},
         "roofline": {"bound": "hbm", "achieved": head["attn_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["hbm_frac"], "traffic": None,
+                     "frac": head["hbm_frac"], "traffic": profiled_traffic(args.ctx),
+                     "traffic_source": "profiles/attn_decode_llama8b_32k.txt (rocprofv3 FETCH_SIZE x 2.0 + "
+                                       "WRITE_SIZE x 1.0, factors from a 256 MiB copy)",
                      "kernel": "bchip attention (rows=1 decode)",
                      "bytes_per_launch": head["attn_bytes_per_launch"], "launch_us": head["attn_launch_us"]},
         "cpu_baseline": cpu,
