@@ -36,7 +36,6 @@
 namespace bchip {
 
 // f16 per row of the transposed V tile in LDS: 64 keys + 4 pad (8-byte aligned rows).
-constexpr int VTS = BLK + 4;
 
 // Softmax state of the lane's slot over NDT output tiles of 16 dims.
 template <int NDT>
@@ -94,12 +93,29 @@ __device__ __forceinline__ float tile_max(float m) {
 // The V^T operand of one PV MFMA: lane (g, n) holds V[key(g, j)][16*dt + n] for the
 // k-dimension order key(g, j) = 32*kc + 16*(j/4) + 4*g + j%4, the order in which this
 // lane holds P^T after the score MFMAs.
-__device__ __forceinline__ half8 v_operand(const f16* __restrict__ vt, int dt, int kc, int g, int n) {
-    const f16* row = vt + (16 * dt + n) * VTS + 32 * kc + 4 * g;
-    half4 a = *(const half4*)row;
-    half4 b = *(const half4*)(row + 16);
+// V tiles sit in LDS row-major ([key][dims], stride VS halves) and reach the MFMA A
+// operand of O^T = V^T P^T through gfx950's transposing LDS read: within each 16-lane
+// group, source lane j names row kbase + j/4, dims c0 + 4(j%4) .. +3, and result lane i
+// receives dims c0 + i of rows kbase .. kbase+3. Lane (n, g) thus holds V[key][16dt + n] for
+// keys 32kc + 4g + 0..3 (first half) and 32kc + 16 + 4g + 0..3 (second half): the key order
+// of the P^T operand built from S^T's registers.
+__device__ __forceinline__ half4 lds_tr4(const f16* p) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+    return __builtin_bit_cast(half4, v);
+}
+
+template <int VS>
+__device__ __forceinline__ half8 v_operand(const f16* __restrict__ vl, int dt, int kc, int g, int j) {
+    const f16* src = vl + (32 * kc + 4 * g + (j >> 2)) * VS + 16 * dt + 4 * (j & 3);
+    const half4 a = lds_tr4(src), b = lds_tr4(src + 16 * VS);
     return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
+
+// Row stride (halves) of a V tile of dw dims in LDS: a multiple of 16 halves with an odd
+// count of 32-byte units, so that the four rows one transposing read takes per 16 lanes,
+// and the eight rows of each 32-lane half, fall on distinct banks.
+constexpr int v_stride(int dw) { return ((dw / 16) & 1) ? dw : dw + 16; }
 
 // One block of 64 list entries [key0, key0+64) for NT tiles of one wave.
 // kop(kt, c) gives the K operand of key tile kt (keys key0+16kt..) and hd chunk c:
@@ -164,7 +180,7 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
     for (int dt = 0; dt < HD / 16; dt++)
 #pragma unroll
         for (int kc = 0; kc < 2; kc++) {
-            half8 a = v_operand(vt, dt, kc, g, n);
+            half8 a = v_operand<v_stride(HD)>(vt, dt, kc, g, n);
 #pragma unroll
             for (int t = 0; t < NT; t++) s[t].o[dt] = mfma16(a, pb[t][kc], s[t].o[dt]);
         }
@@ -200,10 +216,10 @@ __device__ __forceinline__ half8 q_operand(const float* __restrict__ qrow, uint3
     return half8{(f16)a.x, (f16)a.y, (f16)a.z, (f16)a.w, (f16)b.x, (f16)b.y, (f16)b.z, (f16)b.w};
 }
 
-// Writes the 8 f16 values of key kl, dims d0..d0+7, into the transposed tile vt.
-__device__ __forceinline__ void vt_store(f16* __restrict__ vt, int kl, uint32_t d0, half8 v) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) vt[(d0 + j) * VTS + kl] = v[j];
+// Writes the 8 f16 values of key kl, dims d0..d0+7, into the row-major V tile vl.
+template <int VS>
+__device__ __forceinline__ void v_store(f16* __restrict__ vl, int kl, uint32_t d0, half8 v) {
+    *(half8*)&vl[kl * VS + d0] = v;
 }
 
 // Position of the k-th set bit of (lo, hi), k < popcount.
@@ -240,7 +256,8 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     constexpr int KPI = 64 / LPK;                    // keys per V load
     constexpr int NVL = BLK / KPI;                   // V loads per block
     constexpr int NKC = HD / 32;                     // K loads per block (hd chunks)
-    __shared__ __attribute__((aligned(16))) f16 vt[4][DW * VTS];
+    constexpr int VSW = v_stride(DW);
+    __shared__ __attribute__((aligned(16))) f16 vt[4][BLK * VSW];
     __shared__ float red[2][2][4][16];               // [parity][max, sum][key tile][slot]
     __shared__ __attribute__((aligned(8))) half4 pt[2][4][4][16];  // [parity][key tile][g][slot]
     __shared__ __attribute__((aligned(16))) half8 qs[NKC][64];     // Q^T operands by lane
@@ -354,7 +371,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
         if (g == 0) red[par][0][w][n] = tm;
         if (pv) {
 #pragma unroll
-            for (int i = 0; i < NVL; i++) vt_store(vt[w], i * KPI + lane / LPK, 8 * (lane % LPK), vr[i].get());
+            for (int i = 0; i < NVL; i++) v_store<VSW>(vt[w], i * KPI + lane / LPK, 8 * (lane % LPK), vr[i].get());
         }
         __syncthreads();
         const float mx = fmaxf(fmaxf(red[par][0][0][n], red[par][0][1][n]), fmaxf(red[par][0][2][n], red[par][0][3][n]));
@@ -386,7 +403,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
                 for (int kc2 = 0; kc2 < 2; kc2++) {
                     const half4 a = pt[par][2 * kc2][g][n], b = pt[par][2 * kc2 + 1][g][n];
                     const half8 pb = half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-                    o = mfma16(v_operand(vt[w], dt, kc2, g, n), pb, o);
+                    o = mfma16(v_operand<VSW>(vt[w], dt, kc2, g, n), pb, o);
                 }
                 cs.o[dt] = o;
             }
@@ -530,7 +547,7 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
     constexpr int LOADS = BLK * LPR / NTH;  // row loads per thread per block (K and V each)
     static_assert(BLK * LPR % NTH == 0, "block loads must divide over the threads");
     __shared__ __attribute__((aligned(16))) f16 kl[2][BLK * KS];
-    __shared__ __attribute__((aligned(16))) f16 vt[2][HD * VTS];
+    __shared__ __attribute__((aligned(16))) f16 vt[2][BLK * v_stride(HD)];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
@@ -594,7 +611,7 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
             int kr = e / LPR;
             uint32_t hd0 = 8 * (e % LPR);
             *(half8*)&kl[stage][kr * KS + hd0] = kpre[i].get();
-            vt_store(vt[stage], kr, hd0, vpre[i].get());
+            v_store<v_stride(HD)>(vt[stage], kr, hd0, vpre[i].get());
         }
     };
 
