@@ -267,10 +267,10 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     const bool pv = w * DTW < NDT;  // waves with an hd slice (all but for hd <= 32)
     const uint32_t d0 = 16 * DTW * w;
     const uint32_t hd = p.hd, kvd = p.nkv * hd;
-    const bool valid = (uint32_t)n < p.G;
     const KVT* zp = (const KVT*)p.zero;
 
-    // One unit per workgroup, in (item, chunk, KV head) order: the KV heads of one chunk
+    // One unit per workgroup (multi-row lists: tree rows and short lines), in (item, chunk,
+    // KV head) order: the KV heads of one chunk
     // read one stretch of the cache together. Consecutive workgroups go to the 8 XCDs in
     // turn, so the KV head turns with the chunk (j + c) to give every XCD a mix of heads:
     // a fixed head per XCD leaves the XCDs whose head's cache columns map to busier HBM
@@ -281,9 +281,14 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     const Item I = p.items[it];
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = (rem % p.nkv + c) % p.nkv;
     const size_t cu = (size_t)I.unit0 + (size_t)c * p.nkv + kvh;
+    // Slot n of an item is row I.row + n / G, head kvh * G + n % G (an item holds nrows
+    // consecutive rows of a line, or one tree row); row I.row + j sees I.len + j list
+    // entries.
+    const uint32_t srow = n / p.G, shead = kvh * p.G + n % p.G;
+    const bool valid = srow < I.nrows;
     const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
     const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
-    uint32_t len = I.len;
+    uint32_t len = I.len + I.nrows - 1;  // the longest list among the item's rows
     if constexpr (TREE) {
         const uint32_t lo = p.masks[2 * I.row], hi = p.masks[2 * I.row + 1];
         const uint32_t ntail = __popc(lo) + __popc(hi);
@@ -291,6 +296,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
         if ((uint32_t)tid < ntail) tail[tid] = p.base + nth_set_bit(lo, hi, tid);
         __syncthreads();
     }
+    const uint32_t lane_len = TREE ? len : I.len + (valid ? srow : 0u);  // this slot's list
     const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, len);
 
     // Cache slot of list entry k, or ok = false for entries past the list (and for tree
@@ -332,7 +338,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     constexpr int QPW = (NKC + 3) / 4;
     float4 qa[QPW], qb[QPW];
     {
-        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * p.G + (valid ? n : 0)) * hd;
+        const float* qrow = p.q + ((size_t)(I.row + (valid ? srow : 0u)) * p.nh + (valid ? shead : 0u)) * hd;
 #pragma unroll
         for (int j = 0; j < QPW; j++) {
             const uint32_t c2 = w + 4 * j, hd0 = 32 * c2 + 8 * g;
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
         for (int i = 0; i < 4; i++) {
             const uint32_t k = key0 + 16 * w + 4 * g + i;
             const float v = st[i] * p.sc;
-            x[i] = (k < len) ? v : -INFINITY;
+            x[i] = (k < lane_len) ? v : -INFINITY;
             tm = fmaxf(tm, x[i]);
         }
         tm = tile_max(tm);
@@ -424,7 +430,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     }
     if (!valid || !pv) return;
     if (I.nchunk == 1) {
-        float* orow = p.out + ((size_t)I.row * p.nh + kvh * p.G + n) * hd;
+        float* orow = p.out + ((size_t)(I.row + srow) * p.nh + shead) * hd;
 #pragma unroll
         for (int dt = 0; dt < DTW; dt++) {
             const uint32_t d = d0 + 16 * dt + 4 * g;
@@ -435,6 +441,182 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     } else {
         store_state(cs, p.part_o + (cu * 16 + n) * HD, p.part_ml + (cu * 16 + n) * 2, d0, hd, g,
                     w == 0 && g == 0);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// One-row kernel (decode steps and ragged batches of them). A one-row list is bound only to
+// be deterministic and within rounding of the same row in a batch, so it need not share the
+// multi-row arithmetic: each wave streams one (chunk, KV head) unit alone, in blocks of 32
+// entries, with no barrier and no exchange between waves. Lane (n, g) holds slot n (query
+// head kvh * G + n) of keys 4g..4g+3 of each 16-key tile; the block's max and sum cross
+// the four lane groups by permlane swaps, which hand every lane the pair (x[l], x[l^16]) or
+// (x[l], x[l^32]) in the same order. V goes through the wave's own LDS rows and comes back
+// transposed. The four waves of a workgroup take consecutive units: four KV heads of one
+// chunk, so a workgroup reads whole stretches of cache rows together.
+constexpr int RB = 32;  // list entries per block of the one-row kernel
+
+__device__ __forceinline__ float xmax16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xsum16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xsum32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int HD, typename KVT>
+__global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) {
+    constexpr int NKC = HD / 32;        // hd chunks of a score MFMA
+    constexpr int NDT = HD / 16;        // output tiles of 16 dims
+    constexpr int VS = v_stride(HD);    // LDS row stride of V (halves)
+    constexpr int VLR = HD / 8;         // lanes per V row (8 elements each)
+    constexpr int VRI = 64 / VLR;       // V rows per load
+    constexpr int NVL = RB / VRI;       // V loads per block
+    __shared__ __attribute__((aligned(16))) f16 vl[4][RB * VS];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t u = blockIdx.x * 4u + w;  // this wave's unit
+    if (u >= p.nunits) return;               // no barrier below: a wave may leave alone
+    uint32_t it = 0;
+    while (it + 1 < p.nitems && u >= p.items[it + 1].unit0) it++;
+    const Item I = p.items[it];
+    const uint32_t hd = p.hd, kvd = p.nkv * hd;
+    const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = rem % p.nkv;
+    const uint32_t len = I.len, kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, len);
+    const bool valid = (uint32_t)n < p.G;
+    const KVT* zp = (const KVT*)p.zero;
+    const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
+    const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
+
+    // Q^T operands (B of the score MFMAs), straight into registers.
+    half8 qb[NKC];
+    {
+        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * p.G + (valid ? n : 0)) * hd;
+        float4 qa[NKC], qc[NKC];
+#pragma unroll
+        for (int c2 = 0; c2 < NKC; c2++) {
+            const uint32_t hd0 = 32 * c2 + 8 * g;
+            const float* src = (valid && hd0 < hd) ? qrow + hd0 : (const float*)p.zero;
+            qa[c2] = *(const float4*)src;
+            qc[c2] = *(const float4*)(src + 4);
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < NKC; c2++)
+            qb[c2] = half8{(f16)qa[c2].x, (f16)qa[c2].y, (f16)qa[c2].z, (f16)qa[c2].w,
+                           (f16)qc[c2].x, (f16)qc[c2].y, (f16)qc[c2].z, (f16)qc[c2].w};
+    }
+    auto load_block = [&](uint32_t key0, Raw<KVT> (&kr)[2][NKC], Raw<KVT> (&vr)[NVL]) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint32_t key = key0 + 16 * t + n;
+            const KVT* row = kc + (size_t)(key < kb1 ? key : 0u) * kvd;
+#pragma unroll
+            for (int c2 = 0; c2 < NKC; c2++) {
+                const uint32_t hd0 = 32 * c2 + 8 * g;
+                kr[t][c2].load((key < kb1 && hd0 < hd) ? row + hd0 : zp);
+            }
+        }
+        const uint32_t d = 8 * (lane % VLR);
+#pragma unroll
+        for (int i = 0; i < NVL; i++) {
+            const uint32_t key = key0 + i * VRI + lane / VLR;
+            vr[i].load((key < kb1 && d < hd) ? vc + (size_t)key * kvd + d : zp);
+        }
+    };
+    f32x4 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    f16* vw = vl[w];
+    auto compute_block = [&](uint32_t key0, const Raw<KVT> (&kr)[2][NKC], const Raw<KVT> (&vr)[NVL]) {
+#pragma unroll
+        for (int i = 0; i < NVL; i++) v_store<VS>(vw, i * VRI + lane / VLR, 8 * (lane % VLR), vr[i].get());
+        f32x4 st[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c2 = 0; c2 < NKC; c2++) st[t] = mfma16(kr[t][c2].get(), qb[c2], st[t]);
+        }
+        float x[2][4], mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t k = key0 + 16 * t + 4 * g + i;
+                x[t][i] = (k < kb1) ? st[t][i] * p.sc : -INFINITY;
+                mx = fmaxf(mx, x[t][i]);
+            }
+        mx = xmax32(xmax16(mx));
+        const float mn = fmaxf(m, mx);
+        const float ms = (mn == -INFINITY) ? 0.0f : mn;
+        const float corr = exp2_hw(m - ms);
+        half8 pb;
+        float ts = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const f16 e = (f16)exp2_hw(x[t][i] - ms);
+                ts = ts + (float)e;
+                pb[4 * t + i] = e;
+            }
+        ts = xsum32(xsum16(ts));
+        l = l * corr + ts;
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) o[dt] = mfma16(v_operand<VS>(vw, dt, 0, g, n), pb, o[dt] * corr);
+    };
+    // Two register sets in turn where they fit (f16, hd <= 128): the next block loads while
+    // this one computes. Wider rows load and compute one block at a time; their eight
+    // resident waves per CU still overlap one another.
+    if constexpr (sizeof(KVT) == 2 && HD <= 128) {
+        Raw<KVT> kA[2][NKC], vA[NVL], kB[2][NKC], vB[NVL];
+        load_block(kb0, kA, vA);
+        for (uint32_t key0 = kb0;;) {
+            load_block(key0 + RB, kB, vB);
+            compute_block(key0, kA, vA);
+            key0 += RB;
+            if (key0 >= kb1) break;
+            load_block(key0 + RB, kA, vA);
+            compute_block(key0, kB, vB);
+            key0 += RB;
+            if (key0 >= kb1) break;
+        }
+    } else {
+        Raw<KVT> kA[2][NKC], vA[NVL];
+        for (uint32_t key0 = kb0;;) {
+            load_block(key0, kA, vA);
+            compute_block(key0, kA, vA);
+            key0 += RB;
+            if (key0 >= kb1) break;
+        }
+    }
+    if (!valid) return;
+    if (I.nchunk == 1) {
+        float* orow = p.out + ((size_t)I.row * p.nh + kvh * p.G + n) * hd;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const uint32_t d = 16 * dt + 4 * g;
+            if (d < hd) *(float4*)(orow + d) = float4{o[dt][0] / l, o[dt][1] / l, o[dt][2] / l, o[dt][3] / l};
+        }
+    } else {
+        const size_t at = (size_t)u * 16 + n;  // u is the canonical unit0 + c * nkv + kvh
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const uint32_t d = 16 * dt + 4 * g;
+            if (d < hd) *(float4*)(p.part_o + at * HD + d) = float4{o[dt][0], o[dt][1], o[dt][2], o[dt][3]};
+        }
+        if (g == 0) *(float2*)(p.part_ml + at * 2) = float2{m, l};
     }
 }
 
@@ -676,26 +858,19 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// The left fold of split chunks, in chunk order, then O / L: one wave per (output slot,
-// slice of 64 dims). Chunk c's fold weights are a_c = 2^(M_{c-1} - M_c) and
-// b_c = 2^(m_c - M_c), with M_c the running maximum, exactly as fold() computes them; the
-// running maxima are a prefix max, so all weights are computed at once and only
-// O = O*a_c + o_c*b_c (and the same for L) runs chunk by chunk, from partials staged in LDS
-// by loads that are all in flight together.
-constexpr int CMB_PASS = 1024;  // chunks whose weights are computed at once
-constexpr int CMB_STAGE = 128;  // chunks of partial values staged at once
-constexpr int CMB_BATCH = 8;    // recurrence steps whose operands are read ahead
+// Left fold of chunk states, R <- fold(R, c) for c = 0, 1, ... in chunk order, from a
+// cleared R: the per-element arithmetic of fold(), so a split multi-row call gives the
+// bits of the unsplit one. One thread per (group, slot, 4 dims); each pass issues the
+// loads of CMB_RUN chunk states before the first fold step uses them.
+constexpr int CMB_RUN = 16;
 
 template <int HD>
-__global__ __launch_bounds__(64) void attn_combine(const CombineParams p) {
-    __shared__ float sm[CMB_PASS], sx[CMB_PASS], sa[CMB_PASS], sb[CMB_PASS], sl[CMB_PASS];
-    __shared__ __attribute__((aligned(16))) float so[CMB_STAGE * 64];
-    const int lane = threadIdx.x;
-    const uint32_t hd = p.hd;
-    const uint32_t nslice = (hd + 63) / 64;
-    const uint32_t slice = blockIdx.x % nslice, rest = blockIdx.x / nslice;
-    const uint32_t grp = rest / p.slots_out, slot = rest % p.slots_out;
+__global__ __launch_bounds__(256) void attn_combine(const CombineParams p) {
+    const uint32_t nd4 = p.hd / 4;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t d4 = t % nd4, rest = t / nd4;
+    const uint32_t slot = rest % p.slots_out, grp = rest / p.slots_out;
+    if (grp >= p.ngroups) return;
     uint32_t unit0, nchunk, r, h, step;  // chunk c's state is unit unit0 + c * step
     if (p.shared) {
         const uint32_t kvh = grp / p.nrb, rbi = grp % p.nrb;
@@ -708,89 +883,39 @@ __global__ __launch_bounds__(64) void attn_combine(const CombineParams p) {
         step = 1;
     } else {  // decode kernel states, in (item, chunk, KV head) order
         const uint32_t item = grp / p.nkv, kvh = grp % p.nkv;
-        r = p.items[item].row;
-        h = kvh * p.G + slot;
-        unit0 = p.items[item].unit0 + kvh;
-        nchunk = p.items[item].nchunk;
+        const Item& I = p.items[item];
+        if (slot / p.G >= I.nrows || I.nchunk == 1) return;  // one chunk: written directly
+        r = I.row + slot / p.G;
+        h = kvh * p.G + slot % p.G;
+        unit0 = I.unit0 + kvh;
+        nchunk = I.nchunk;
         step = p.nkv;
-        if (nchunk == 1) return;  // the decode kernel wrote this row's output itself
     }
-    const uint32_t stride = p.slots;  // partial slots per unit
-    const uint32_t dbase = 64 * slice;
-    const uint32_t d = dbase + lane;
-    float Mrun = -INFINITY, L = 0.0f, O = 0.0f;
-    for (uint32_t cb = 0; cb < nchunk; cb += CMB_PASS) {
-        const uint32_t cnt = min((uint32_t)CMB_PASS, nchunk - cb);
-        for (uint32_t c = lane; c < cnt; c += 64) {
-            const float2 ml = *(const float2*)(p.part_ml + ((size_t)unit0 + (size_t)(cb + c) * step) * stride * 2 + slot * 2);
-            sm[c] = ml.x;
-            sl[c] = ml.y;
-        }
-        __syncthreads();
-        // Inclusive prefix max over the pass: each lane a segment, then across lanes.
-        const uint32_t seg = (cnt + 63) / 64, s0 = lane * seg, s1 = min(s0 + seg, cnt);
-        float run = -INFINITY;
-        for (uint32_t c = s0; c < s1; c++) {
-            run = fmaxf(run, sm[c]);
-            sx[c] = run;
-        }
-        float incl = run;
+    const size_t stride = p.slots;  // partial slots per unit
+    float M = -INFINITY, L = 0.0f;
+    float4 O = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t cb = 0; cb < nchunk; cb += CMB_RUN) {
+        float2 ml[CMB_RUN];
+        float4 o[CMB_RUN];
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float t = __shfl_up(incl, off);
-            if (lane >= off) incl = fmaxf(incl, t);
+        for (int j = 0; j < CMB_RUN; j++) {
+            const uint32_t c = min(cb + j, nchunk - 1);
+            const size_t at = ((size_t)unit0 + (size_t)c * step) * stride + slot;
+            ml[j] = *(const float2*)(p.part_ml + at * 2);
+            o[j] = *(const float4*)(p.part_o + at * HD + 4 * d4);
         }
-        float excl = __shfl_up(incl, 1);
-        if (lane == 0) excl = -INFINITY;
-        for (uint32_t c = s0; c < s1; c++) sx[c] = fmaxf(excl, sx[c]);
-        __syncthreads();
-        for (uint32_t c = lane; c < cnt; c += 64) {
-            const float Mprev = c == 0 ? Mrun : fmaxf(Mrun, sx[c - 1]);
-            float a, b, mn;
-            merge_coef(Mprev, sm[c], a, b, mn);
-            sa[c] = a;
-            sb[c] = b;
-        }
-        __syncthreads();
-        for (uint32_t st0 = 0; st0 < cnt; st0 += CMB_STAGE) {
-            const uint32_t k = min((uint32_t)CMB_STAGE, cnt - st0);
-            // 16 float4 per chunk slice: k * 16 loads over 64 lanes, issued before any store.
-            float4 v[CMB_STAGE * 16 / 64];
 #pragma unroll
-            for (int i = 0; i < CMB_STAGE * 16 / 64; i++) {
-                const uint32_t e = i * 64 + lane, cc = e / 16, q = 4 * (e % 16);
-                const float* src = (cc < k && dbase + q < hd)
-                                       ? p.part_o + (((size_t)unit0 + (size_t)(cb + st0 + cc) * step) * stride + slot) * HD + dbase + q
-                                       : (const float*)p.zero;
-                v[i] = *(const float4*)src;
+        for (int j = 0; j < CMB_RUN; j++) {
+            if (cb + j < nchunk) {
+                float a, b, mn;
+                merge_coef(M, ml[j].x, a, b, mn);
+                L = L * a + ml[j].y * b;
+                O = float4{O.x * a + o[j].x * b, O.y * a + o[j].y * b, O.z * a + o[j].z * b, O.w * a + o[j].w * b};
+                M = mn;
             }
-#pragma unroll
-            for (int i = 0; i < CMB_STAGE * 16 / 64; i++) *(float4*)&so[(i * 64 + lane) * 4] = v[i];
-            __syncthreads();
-            for (uint32_t c0 = 0; c0 < k; c0 += CMB_BATCH) {
-                float ba[CMB_BATCH], bb[CMB_BATCH], bl[CMB_BATCH], bo[CMB_BATCH];
-#pragma unroll
-                for (int j = 0; j < CMB_BATCH; j++) {
-                    const uint32_t c = min(c0 + j, k - 1);
-                    ba[j] = sa[st0 + c];
-                    bb[j] = sb[st0 + c];
-                    bl[j] = sl[st0 + c];
-                    bo[j] = so[c * 64 + lane];
-                }
-#pragma unroll
-                for (int j = 0; j < CMB_BATCH; j++) {
-                    if (c0 + j < k) {
-                        L = L * ba[j] + bl[j] * bb[j];
-                        O = O * ba[j] + bo[j] * bb[j];
-                    }
-                }
-            }
-            __syncthreads();
         }
-        Mrun = fmaxf(Mrun, sx[cnt - 1]);
-        __syncthreads();
     }
-    if (d < hd) p.out[((size_t)r * p.nh + h) * hd + d] = O / L;
+    *(float4*)(p.out + ((size_t)r * p.nh + h) * p.hd + 4 * d4) = float4{O.x / L, O.y / L, O.z / L, O.w / L};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -798,24 +923,25 @@ __global__ __launch_bounds__(64) void attn_combine(const CombineParams p) {
 
 static uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
-// Chunk of a one-row call with nkv KV heads: the smallest power of two of at least one block
-// that cuts the list into at most 512 / nkv chunks (at least 1, at most 256, what
-// attn_decode_fold takes): about two units of several blocks per CU, so that the grid is
-// resident at once and every CU streams to the end without a second dispatch round.
-// Any u32 list length fits (2^24 * 256 = 2^32).
+// Chunk of a one-row list with nkv KV heads: the smallest power of two of at least two of
+// the one-row kernel's blocks that cuts the list into at most 2048 / nkv chunks (at least
+// 1, at most 8 * FOLD_RUNS = 256, what attn_decode_fold takes). A long step then has about
+// 2048 wave units, eight resident per CU, all issuing their loads from the start. Any u32
+// list length fits (2^24 * 256 = 2^32).
 uint32_t decode_chunk(uint64_t len, uint32_t nkv) {
-    uint64_t most = 512 / (nkv ? nkv : 1);
+    uint64_t most = 2048 / (nkv ? nkv : 1);
     if (most < 1) most = 1;
     if (most > 8 * FOLD_RUNS) most = 8 * FOLD_RUNS;
-    uint32_t c = BLK;
+    uint32_t c = 2 * RB;
     while ((len + c - 1) / c > most && c < (1u << 24)) c <<= 1;
     return c;
 }
 
 template <int HD>
-static hipError_t launch_combine_t(const CombineParams& cp, uint32_t groups, hipStream_t s) {
-    const uint32_t nslice = (cp.hd + 63) / 64;
-    hipLaunchKernelGGL((attn_combine<HD>), dim3(groups * cp.slots_out * nslice), dim3(64), 0, s, cp);
+static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s) {
+    cp.ngroups = groups;
+    const uint64_t threads = (uint64_t)groups * cp.slots_out * (cp.hd / 4);
+    hipLaunchKernelGGL((attn_combine<HD>), dim3(ceil_div(threads, 256)), dim3(256), 0, s, cp);
     return hipGetLastError();
 }
 
@@ -841,16 +967,17 @@ static int pad_hd(uint32_t hd) {
     }
 
 template <int HD>
-static hipError_t launch_combine_t(const CombineParams& cp, uint32_t groups, hipStream_t s);
+static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s);
 
 template <int HD, typename KVT>
-static hipError_t launch_decode_t(DirectParams& dp, uint32_t folds, const CombineParams* left, hipStream_t s) {
+static hipError_t launch_decode_t(DirectParams& dp, uint32_t folds, CombineParams* left, hipStream_t s) {
     const dim3 block(256);
-    const dim3 grid(dp.nunits);
     if (dp.tree)
-        hipLaunchKernelGGL((attn_decode<HD, KVT, true>), grid, block, 0, s, dp);
+        hipLaunchKernelGGL((attn_decode<HD, KVT, true>), dim3(dp.nunits), block, 0, s, dp);
+    else if (left)
+        hipLaunchKernelGGL((attn_decode<HD, KVT, false>), dim3(dp.nunits), block, 0, s, dp);
     else
-        hipLaunchKernelGGL((attn_decode<HD, KVT, false>), grid, block, 0, s, dp);
+        hipLaunchKernelGGL((attn_decode_row<HD, KVT>), dim3(ceil_div(dp.nunits, 4)), block, 0, s, dp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || folds == 0) return e;
     if (left) return launch_combine_t<HD>(*left, dp.nitems * dp.nkv, s);
@@ -877,6 +1004,7 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
     dp.nitems = nitems;
     uint32_t units = 0, folds = 0;
     const uint32_t nslice = (a.hd + FOLD_DIMS - 1) / FOLD_DIMS;
+    const int hdp = pad_hd(a.hd);
     for (uint32_t i = 0; i < nitems; i++) {
         Item& I = dp.items[i];
         I = items[i];
@@ -886,7 +1014,6 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
         if (a.rows == 1 && I.nchunk > 8 * FOLD_RUNS) return hipErrorInvalidValue;  // decode_chunk keeps to 256
     }
     dp.nunits = units;
-    const int hdp = pad_hd(a.hd);
     hipError_t e = ws.reserve((size_t)units * 16, (size_t)hdp);
     if (e != hipSuccess) return e;
     dp.part_o = ws.o;
@@ -905,7 +1032,7 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
         cp.hd = a.hd;
         cp.G = dp.G;
         cp.slots = 16;
-        cp.slots_out = dp.G;
+        cp.slots_out = 16;
         cp.shared = 0;
         cp.nitems = nitems;
         for (uint32_t i = 0; i < nitems; i++) cp.items[i] = dp.items[i];

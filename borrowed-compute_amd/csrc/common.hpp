@@ -41,9 +41,10 @@ struct Item {
     uint32_t unit0;  // first unit of this item in the launch
     uint32_t nchunk; // chunks of this row's list (an upper bound for tree rows)
     uint32_t chunk;  // list entries per chunk (multiple of BLK)
-    uint32_t pad_;
+    uint32_t nrows;  // consecutive line rows in this item (1 for decode and tree rows)
     uint64_t kvoff;  // slot offset of the row's cache (ragged pools), else 0
 };
+
 
 // zero: a device page of zeros that lanes with nothing to read load from.
 struct DirectParams {
@@ -94,6 +95,7 @@ struct CombineParams {
     // decode launches: one group per (item, KV head); shared: one per (KV head, row block)
     uint32_t shared;
     uint32_t rows, rb, nrb, nchunk; // shared launches
+    uint32_t ngroups;  // groups in the launch
     uint32_t nitems;
     Item items[MAX_ITEMS];
 };

@@ -136,6 +136,8 @@ PREFILL = [
     (40, 3, 8, 8, 256, bchip.F16),
     (8, 4096, 64, 8, 128, bchip.F16),   # config 5 verify: split across chunks
     (8, 1000, 16, 1, 128, bchip.F16),
+    (5, 600, 14, 2, 64, bchip.F32),     # short line, G = 7: units of 2 rows, f32 cache
+    (3, 2000, 28, 4, 128, bchip.F16),   # short line over 8 chunks, G = 7
 ]
 
 
