@@ -75,19 +75,38 @@ __device__ __forceinline__ void fold(State<NDT>& R, const State<NDT>& c) {
     R.m = mn;
 }
 
-// Sum of one slot's values over a 16-key tile: the lane's four keys in order, then the
-// four lane groups (l, l^16, l^32, l^48) pairwise. A block's sum adds the four tiles'
-// sums in tile order.
-__device__ __forceinline__ float tile_sum(float s) {
-    s = s + __shfl_xor(s, 16);
-    s = s + __shfl_xor(s, 32);
-    return s;
+// The two lane-group crossings of a 16-key tile: permlane swaps hand each lane the pair
+// (x[l], x[l^16]) (or l^32) from the lower and the upper lane, in that order on both lanes,
+// so a max or a sum of the pair is the same bits on both. A slot's sum over a tile is its
+// lane's four keys in order, then the pairs across l^16, then across l^32; a block's sum
+// adds the four tiles' sums in tile order.
+__device__ __forceinline__ float xmax16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float xmax32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xsum16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xsum32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float tile_sum(float s) { return xsum32(xsum16(s)); }
+__device__ __forceinline__ float tile_max(float m) { return xmax32(xmax16(m)); }
 
-__device__ __forceinline__ float tile_max(float m) {
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
-    return m;
+// O <- O * corr for a wave's slots, skipped when every slot's max held (corr == 1 exactly,
+// and x * 1 == x): in a long list the running max rarely moves, and the rescale is VALU
+// work on every output register.
+template <int NDT>
+__device__ __forceinline__ void rescale(f32x4 (&o)[NDT], float corr) {
+    if (__all(corr == 1.0f)) return;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) o[dt] = o[dt] * corr;
 }
 
 // The V^T operand of one PV MFMA: lane (g, n) holds V[key(g, j)][16*dt + n] for the
@@ -124,7 +143,7 @@ constexpr int v_stride(int dw) { return ((dw / 16) & 1) ? dw : dw + 16; }
 template <int HD, int NT, typename KOp>
 __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 (&qb)[NT][HD / 32], KOp kop,
                                            const f16* __restrict__ vt, uint32_t key0,
-                                           const uint32_t (&len)[NT], float sc) {
+                                           const uint32_t (&len)[NT]) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, n = lane & 15;
     f32x4 st[NT][4];
@@ -142,16 +161,18 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
     half8 pb[NT][2];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
+        // Scores are in log2 units already (the scale rides in Q). Entries at or past a
+        // slot's list length are masked; a block every slot sees whole skips the test.
         float x[4][4];
         float mx = -INFINITY;
+        const bool whole = __all(key0 + BLK <= len[t]);
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             float tm = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                uint32_t k = key0 + 16 * kt + 4 * g + i;
-                float v = st[t][kt][i] * sc;
-                x[kt][i] = (k < len[t]) ? v : -INFINITY;
+                const uint32_t k = key0 + 16 * kt + 4 * g + i;
+                x[kt][i] = (whole || k < len[t]) ? st[t][kt][i] : -INFINITY;
                 tm = fmaxf(tm, x[kt][i]);
             }
             mx = fmaxf(mx, tile_max(tm));
@@ -173,8 +194,7 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
         }
         s[t].l = s[t].l * corr + ps;
         s[t].m = mn;
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; dt++) s[t].o[dt] = s[t].o[dt] * corr;
+        rescale(s[t].o, corr);
     }
 #pragma unroll
     for (int dt = 0; dt < HD / 16; dt++)
@@ -210,10 +230,17 @@ struct Raw<float> {
     }
 };
 
-__device__ __forceinline__ half8 q_operand(const float* __restrict__ qrow, uint32_t hd0, uint32_t hd, bool ok) {
+// 8 elements of a Q row times sc (the attention scale times log2(e), so that scores come
+// out of the MFMA in exp2 units), rounded to f16: the B operand of the score MFMAs.
+__device__ __forceinline__ half8 q_scaled(float4 a, float4 b, float sc) {
+    return half8{(f16)(a.x * sc), (f16)(a.y * sc), (f16)(a.z * sc), (f16)(a.w * sc),
+                 (f16)(b.x * sc), (f16)(b.y * sc), (f16)(b.z * sc), (f16)(b.w * sc)};
+}
+
+__device__ __forceinline__ half8 q_operand(const float* __restrict__ qrow, uint32_t hd0, uint32_t hd, bool ok, float sc) {
     if (!ok || hd0 >= hd) return half8{0, 0, 0, 0, 0, 0, 0, 0};
     float4 a = *(const float4*)(qrow + hd0), b = *(const float4*)(qrow + hd0 + 4);
-    return half8{(f16)a.x, (f16)a.y, (f16)a.z, (f16)a.w, (f16)b.x, (f16)b.y, (f16)b.z, (f16)b.w};
+    return q_scaled(a, b, sc);
 }
 
 // Writes the 8 f16 values of key kl, dims d0..d0+7, into the row-major V tile vl.
@@ -352,8 +379,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     for (int j = 0; j < QPW; j++) {
         const uint32_t c2 = w + 4 * j;
         if (c2 < (uint32_t)NKC)
-            qs[c2][lane] = half8{(f16)qa[j].x, (f16)qa[j].y, (f16)qa[j].z, (f16)qa[j].w,
-                                 (f16)qb[j].x, (f16)qb[j].y, (f16)qb[j].z, (f16)qb[j].w};
+            qs[c2][lane] = q_scaled(qa[j], qb[j], p.sc);
     }
     __syncthreads();
 
@@ -366,11 +392,11 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++) st = mfma16(kr[c2].get(), qs[c2][lane], st);
         float x[4], tm = -INFINITY;
+        const bool whole = __all(key0 + BLK <= lane_len);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t k = key0 + 16 * w + 4 * g + i;
-            const float v = st[i] * p.sc;
-            x[i] = (k < lane_len) ? v : -INFINITY;
+            x[i] = (whole || k < lane_len) ? st[i] : -INFINITY;
             tm = fmaxf(tm, x[i]);
         }
         tm = tile_max(tm);
@@ -402,9 +428,10 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
         cs.l = cs.l * corr + ps;
         cs.m = mn;
         if (pv) {
+            rescale(cs.o, corr);
 #pragma unroll
             for (int dt = 0; dt < DTW; dt++) {
-                f32x4 o = cs.o[dt] * corr;
+                f32x4 o = cs.o[dt];
 #pragma unroll
                 for (int kc2 = 0; kc2 < 2; kc2++) {
                     const half4 a = pt[par][2 * kc2][g][n], b = pt[par][2 * kc2 + 1][g][n];
@@ -456,23 +483,6 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 // chunk, so a workgroup reads whole stretches of cache rows together.
 constexpr int RB = 32;  // list entries per block of the one-row kernel
 
-__device__ __forceinline__ float xmax16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xmax32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xsum16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xsum32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 template <int HD, typename KVT>
 __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) {
     constexpr int NKC = HD / 32;        // hd chunks of a score MFMA
@@ -511,8 +521,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         }
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++)
-            qb[c2] = half8{(f16)qa[c2].x, (f16)qa[c2].y, (f16)qa[c2].z, (f16)qa[c2].w,
-                           (f16)qc[c2].x, (f16)qc[c2].y, (f16)qc[c2].z, (f16)qc[c2].w};
+            qb[c2] = q_scaled(qa[c2], qc[c2], p.sc);
     }
     auto load_block = [&](uint32_t key0, Raw<KVT> (&kr)[2][NKC], Raw<KVT> (&vr)[NVL]) {
 #pragma unroll
@@ -553,7 +562,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t k = key0 + 16 * t + 4 * g + i;
-                x[t][i] = (k < kb1) ? st[t][i] * p.sc : -INFINITY;
+                x[t][i] = (k < kb1) ? st[t][i] : -INFINITY;
                 mx = fmaxf(mx, x[t][i]);
             }
         mx = xmax32(xmax16(mx));
@@ -573,8 +582,9 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         ts = xsum32(xsum16(ts));
         l = l * corr + ts;
         m = mn;
+        rescale(o, corr);
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) o[dt] = mfma16(v_operand<VS>(vw, dt, 0, g, n), pb, o[dt] * corr);
+        for (int dt = 0; dt < NDT; dt++) o[dt] = mfma16(v_operand<VS>(vw, dt, 0, g, n), pb, o[dt]);
     };
     // Two register sets in turn where they fit (f16, hd <= 128): the next block loads while
     // this one computes. Wider rows load and compute one block at a time; their eight
@@ -758,7 +768,7 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
         ohead[t] = kvh * p.G + gh;
         const float* qrow = p.q + ((size_t)(valid[t] ? r : 0u) * p.nh + (valid[t] ? ohead[t] : 0u)) * hd;
 #pragma unroll
-        for (int c = 0; c < HD / 32; c++) qb[t][c] = q_operand(qrow, 32 * c + 8 * g, hd, valid[t]);
+        for (int c = 0; c < HD / 32; c++) qb[t][c] = q_operand(qrow, 32 * c + 8 * g, hd, valid[t], p.sc);
     }
 
     const KVT* kcb = (const KVT*)p.kc + (size_t)kvh * hd;
@@ -823,7 +833,7 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
         block_step<HD, NT>(
             cs, qb,
             [&](int kt, int c) { return *(const half8*)&kls[(16 * kt + n) * KS + 32 * c + 8 * g]; },
-            vt[stage], key0, len, p.sc);
+            vt[stage], key0, len);
         store_block(stage ^ 1);
         __syncthreads();
         stage ^= 1;
