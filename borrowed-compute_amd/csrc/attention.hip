@@ -138,12 +138,12 @@ constexpr int v_stride(int dw) { return ((dw / 16) & 1) ? dw : dw + 16; }
 
 // One block of 64 list entries [key0, key0+64) for NT tiles of one wave.
 // kop(kt, c) gives the K operand of key tile kt (keys key0+16kt..) and hd chunk c:
-// lane (g, n) holds K[key0 + 16kt + n][32c + 8g .. +8]. vt is V^T of the block in LDS.
+// lane (g, n) holds K[key0 + 16kt + n][32c + 8g .. +8]; vop(dt, kc) gives the V^T operand
+// of output tile dt and key half kc (the order of v_operand).
 // len[t] is the list length of this lane's slot in tile t (entries >= len are masked).
-template <int HD, int NT, typename KOp>
+template <int HD, int NT, typename KOp, typename VOp>
 __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 (&qb)[NT][HD / 32], KOp kop,
-                                           const f16* __restrict__ vt, uint32_t key0,
-                                           const uint32_t (&len)[NT]) {
+                                           VOp vop, uint32_t key0, const uint32_t (&len)[NT]) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, n = lane & 15;
     f32x4 st[NT][4];
@@ -200,7 +200,7 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
     for (int dt = 0; dt < HD / 16; dt++)
 #pragma unroll
         for (int kc = 0; kc < 2; kc++) {
-            half8 a = v_operand<v_stride(HD)>(vt, dt, kc, g, n);
+            half8 a = vop(dt, kc);
 #pragma unroll
             for (int t = 0; t < NT; t++) s[t].o[dt] = mfma16(a, pb[t][kc], s[t].o[dt]);
         }
@@ -833,7 +833,7 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
         block_step<HD, NT>(
             cs, qb,
             [&](int kt, int c) { return *(const half8*)&kls[(16 * kt + n) * KS + 32 * c + 8 * g]; },
-            vt[stage], key0, len);
+            [&](int dt, int kc) { return v_operand<v_stride(HD)>(vt[stage], dt, kc, g, n); }, key0, len);
         store_block(stage ^ 1);
         __syncthreads();
         stage ^= 1;
@@ -926,6 +926,164 @@ __global__ __launch_bounds__(256) void attn_combine(const CombineParams p) {
         }
     }
     *(float4*)(p.out + ((size_t)r * p.nh + h) * p.hd + 4 * d4) = float4{O.x / L, O.y / L, O.z / L, O.w / L};
+}
+
+// ---------------------------------------------------------------------------------------
+// Prefill kernel (f16 caches, hd 128): the shared kernel's slots and arithmetic (block_step
+// per 64-entry block, chunk states folded every 256 entries), with K and V blocks copied
+// HBM -> LDS by the gfx950 direct-to-LDS loads, so that no VGPR holds a block in flight.
+// Each load instruction of a wave fills 1 KB of LDS in lane order: four whole cache rows,
+// lane l taking row 4q + l/16 and 16-byte chunk (l % 16) ^ f(row) of it, so the LDS rows
+// are XOR-swizzled by chunk: K by f = row % 16 (the sixteen rows one score operand read
+// takes sit on distinct banks), V by f = 2 (row % 8) (chunk pairs stay adjacent for the
+// transposing reads, and the eight rows of a 32-lane half fall on distinct banks).
+constexpr int PF_CPR = 16;  // 16-byte chunks per row (hd 128 in f16)
+
+__device__ __forceinline__ uint32_t pf_kswz(uint32_t r) { return r % 16u; }
+__device__ __forceinline__ uint32_t pf_vswz(uint32_t r) { return 2u * (r % 8u); }
+
+// s_waitcnt for "at most N vector memory operations of this wave outstanding" (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maximum).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0xF70);
+}
+
+template <int W, int NT>
+__global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
+    constexpr int HD = 128;
+    constexpr int SL = W * NT * 16;
+    constexpr int NKC = HD / 32, NDT = HD / 16;
+    constexpr int RPI = 64 / PF_CPR;            // cache rows per load instruction
+    constexpr int LPW = BLK / RPI / W;          // load instructions per wave per block (K or V)
+    __shared__ __attribute__((aligned(16))) f16 kl[2][BLK * HD];
+    __shared__ __attribute__((aligned(16))) f16 vl[2][BLK * HD];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t gi_launch = p.split ? blockIdx.x / p.nchunk : blockIdx.x;
+    const uint32_t cs_idx = p.split ? blockIdx.x % p.nchunk : 0u;
+    const uint32_t kvh = gi_launch % p.nkv;
+    const uint32_t rbi = p.nrb - 1u - gi_launch / p.nkv;  // heaviest row blocks first
+    const uint32_t grp = kvh * p.nrb + rbi;
+    const uint32_t r0 = rbi * p.rb;
+    const uint32_t rlast = min(r0 + p.rb, p.rows) - 1u;
+    const uint32_t maxlen = p.pos + rlast + 1u;
+    const uint32_t hd = p.hd, kvd = p.nkv * hd;
+
+    half8 qb[NT][NKC];
+    uint32_t len[NT], orow[NT], ohead[NT];
+    bool valid[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const uint32_t sl = (w * NT + t) * 16 + n;
+        const uint32_t gh = sl / p.rb, rl = sl % p.rb, r = r0 + rl;
+        valid[t] = gh < p.G && r < p.rows;
+        len[t] = valid[t] ? p.pos + r + 1u : 0u;
+        orow[t] = r;
+        ohead[t] = kvh * p.G + gh;
+        const float* qrow = p.q + ((size_t)(valid[t] ? r : 0u) * p.nh + (valid[t] ? ohead[t] : 0u)) * hd;
+#pragma unroll
+        for (int c = 0; c < NKC; c++) qb[t][c] = q_operand(qrow, 32 * c + 8 * g, hd, valid[t], p.sc);
+    }
+
+    const f16* kcb = (const f16*)p.kc + (size_t)kvh * hd;
+    const f16* vcb = (const f16*)p.vc + (size_t)kvh * hd;
+    uint32_t kb0, kb1;
+    if (p.split) {
+        kb0 = cs_idx * CHUNK_MULTI;
+        kb1 = min(kb0 + CHUNK_MULTI, maxlen);
+    } else {
+        kb0 = 0;
+        kb1 = maxlen;
+    }
+    const f16* zp = (const f16*)p.zero;
+    // Block key0 into stage st: this wave's LPW instructions for K and for V (rows past kb1
+    // read the zero page).
+    auto load_block = [&](uint32_t key0, int st) {
+#pragma unroll
+        for (int i = 0; i < LPW; i++) {
+            const uint32_t q = i * W + w;                 // instruction of the block
+            const uint32_t row = q * RPI + lane / PF_CPR, pch = lane % PF_CPR;
+            const uint32_t key = key0 + row;
+            const bool ok = key < kb1;
+            const f16* ks = ok ? kcb + (size_t)key * kvd + 8 * (pch ^ pf_kswz(row)) : zp + 8 * pch;
+            const f16* vs = ok ? vcb + (size_t)key * kvd + 8 * (pch ^ pf_vswz(row)) : zp + 8 * pch;
+            __builtin_amdgcn_global_load_lds((const void*)ks, (__attribute__((address_space(3))) void*)&kl[st][q * RPI * HD], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)&vl[st][q * RPI * HD], 16, 0, 0);
+        }
+    };
+
+    State<NDT> R[NT], cs[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        state_clear(R[t]);
+        state_clear(cs[t]);
+    }
+    int st = 0;
+    load_block(kb0, 0);
+    for (uint32_t key0 = kb0; key0 < kb1; key0 += BLK) {
+        // This block's rows are in (own loads: wait; everyone's: barrier); the barrier also
+        // ends every read of the other stage, which the next block's loads then refill.
+        wait_vm<0>();
+        __syncthreads();
+        load_block(key0 + BLK, st ^ 1);
+        if (key0 != kb0 && key0 % CHUNK_MULTI == 0) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                fold(R[t], cs[t]);
+                state_clear(cs[t]);
+            }
+        }
+        const f16* kls = kl[st];
+        const f16* vls = vl[st];
+        block_step<HD, NT>(
+            cs, qb,
+            [&](int kt, int c) {
+                const uint32_t r = 16 * kt + n, ch = 4 * c + g;
+                return *(const half8*)&kls[r * HD + 8 * (ch ^ pf_kswz(r))];
+            },
+            [&](int dt, int kc) {
+                // transposing read: source lane j of its 16-lane group names row
+                // kbase + j/4, dims 16dt + 4(j%4): chunk 2dt + (j%4)/2, half (j%4)%2
+                const uint32_t r = 32 * kc + 4 * g + (n >> 2), ch = 2 * dt + ((n & 3) >> 1), h = n & 1;
+                const half4 a = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
+                const uint32_t r2 = r + 16;
+                const half4 b = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
+                return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+            },
+            key0, len);
+        st ^= 1;
+    }
+    wait_vm<0>();  // the prefetch past the end (zero page) lands before the workgroup ends
+    if (p.split) {
+        const size_t u = (size_t)grp * p.nchunk + cs_idx;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const uint32_t sl = (w * NT + t) * 16 + n;
+            float* po = p.part_o + (u * SL + sl) * HD;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                const uint32_t d = 16 * dt + 4 * g;
+                *(float4*)(po + d) = float4{cs[t].o[dt][0], cs[t].o[dt][1], cs[t].o[dt][2], cs[t].o[dt][3]};
+            }
+            if (g == 0) *(float2*)(p.part_ml + (u * SL + sl) * 2) = float2{cs[t].m, cs[t].l};
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        fold(R[t], cs[t]);
+        if (!valid[t]) continue;
+        float* o = p.out + ((size_t)orow[t] * p.nh + ohead[t]) * hd;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const uint32_t d = 16 * dt + 4 * g;
+            *(float4*)(o + d) = float4{R[t].o[dt][0] / R[t].l, R[t].o[dt][1] / R[t].l, R[t].o[dt][2] / R[t].l,
+                                       R[t].o[dt][3] / R[t].l};
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1091,7 +1249,13 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     }
     const uint32_t blocks = groups * (sp.split ? sp.nchunk : 1u);
     hipError_t e;
-    if (a.kv_type == 1) {
+    if (a.kv_type == 1 && a.hd == 128) {
+        if (wide)
+            hipLaunchKernelGGL((attn_prefill<8, 1>), dim3(blocks), dim3(512), 0, s, sp);
+        else
+            hipLaunchKernelGGL((attn_prefill<4, 1>), dim3(blocks), dim3(256), 0, s, sp);
+        e = hipGetLastError();
+    } else if (a.kv_type == 1) {
         if (wide) {
             BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, s)));
         } else {
