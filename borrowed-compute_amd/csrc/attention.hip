@@ -102,9 +102,15 @@ __device__ __forceinline__ float tile_max(float m) { return xmax32(xmax16(m)); }
 // O <- O * corr for a wave's slots, skipped when every slot's max held (corr == 1 exactly,
 // and x * 1 == x): in a long list the running max rarely moves, and the rescale is VALU
 // work on every output register.
+// keep_branch() marks a uniform branch's body as having an effect, so the compiler keeps
+// the branch instead of running the body for every wave and selecting (which it otherwise
+// does for short bodies, turning a skipped multiply into an executed one).
+__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+
 template <int NDT>
 __device__ __forceinline__ void rescale(f32x4 (&o)[NDT], float corr) {
     if (__all(corr == 1.0f)) return;
+    keep_branch();
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) o[dt] = o[dt] * corr;
 }
@@ -165,16 +171,23 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
         // slot's list length are masked; a block every slot sees whole skips the test.
         float x[4][4];
         float mx = -INFINITY;
-        const bool whole = __all(key0 + BLK <= len[t]);
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[kt][i] = st[t][kt][i];
+        if (!__all(key0 + BLK <= len[t])) {
+            keep_branch();
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (key0 + 16 * kt + 4 * g + i >= len[t]) x[kt][i] = -INFINITY;
+        }
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             float tm = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t k = key0 + 16 * kt + 4 * g + i;
-                x[kt][i] = (whole || k < len[t]) ? st[t][kt][i] : -INFINITY;
-                tm = fmaxf(tm, x[kt][i]);
-            }
+            for (int i = 0; i < 4; i++) tm = fmaxf(tm, x[kt][i]);
             mx = fmaxf(mx, tile_max(tm));
         }
         float mn = fmaxf(s[t].m, mx);
@@ -392,13 +405,16 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++) st = mfma16(kr[c2].get(), qs[c2][lane], st);
         float x[4], tm = -INFINITY;
-        const bool whole = __all(key0 + BLK <= lane_len);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t k = key0 + 16 * w + 4 * g + i;
-            x[i] = (whole || k < lane_len) ? st[i] : -INFINITY;
-            tm = fmaxf(tm, x[i]);
+        for (int i = 0; i < 4; i++) x[i] = st[i];
+        if (!__all(key0 + BLK <= lane_len)) {
+            keep_branch();
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (key0 + 16 * w + 4 * g + i >= lane_len) x[i] = -INFINITY;
         }
+#pragma unroll
+        for (int i = 0; i < 4; i++) tm = fmaxf(tm, x[i]);
         tm = tile_max(tm);
         if (g == 0) red[par][0][w][n] = tm;
         if (pv) {
@@ -1030,6 +1046,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         __syncthreads();
         load_block(key0 + BLK, st ^ 1);
         if (key0 != kb0 && key0 % CHUNK_MULTI == 0) {
+            keep_branch();
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 fold(R[t], cs[t]);
