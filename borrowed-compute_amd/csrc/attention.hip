@@ -77,9 +77,9 @@ __device__ __forceinline__ void fold(State<NDT>& R, const State<NDT>& c) {
 
 // The two lane-group crossings of a 16-key tile: permlane swaps hand each lane the pair
 // (x[l], x[l^16]) (or l^32) from the lower and the upper lane, in that order on both lanes,
-// so a max or a sum of the pair is the same bits on both. A slot's sum over a tile is its
-// lane's four keys in order, then the pairs across l^16, then across l^32; a block's sum
-// adds the four tiles' sums in tile order.
+// so a max or a sum of the pair is the same bits on both. A slot's sum over a 64-entry block
+// is, per lane, each tile's four keys in order and the four tiles in order, then the pairs
+// across l^16, then across l^32.
 __device__ __forceinline__ float xmax16(float x) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -183,17 +183,19 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
                 for (int i = 0; i < 4; i++)
                     if (key0 + 16 * kt + 4 * g + i >= len[t]) x[kt][i] = -INFINITY;
         }
+        // The block max: the lane's sixteen entries, then across lanes (a max is exact in
+        // any order).
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            float tm = -INFINITY;
+        for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) tm = fmaxf(tm, x[kt][i]);
-            mx = fmaxf(mx, tile_max(tm));
-        }
+            for (int i = 0; i < 4; i++) mx = fmaxf(mx, x[kt][i]);
+        mx = tile_max(mx);
         float mn = fmaxf(s[t].m, mx);
         float ms = (mn == -INFINITY) ? 0.0f : mn;
         float corr = exp2_hw(s[t].m - ms);
-        float ps = 0.0f;
+        // The block sum: per lane, each tile's four entries in order, the tiles in order;
+        // then across lanes (l^16, then l^32).
+        float ls = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             float ts = 0.0f;
@@ -203,8 +205,9 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
                 ts = ts + (float)ph;
                 pb[t][kt >> 1][(kt & 1) * 4 + i] = ph;
             }
-            ps = ps + tile_sum(ts);
+            ls = ls + ts;
         }
+        const float ps = tile_sum(ls);
         s[t].l = s[t].l * corr + ps;
         s[t].m = mn;
         rescale(s[t].o, corr);
@@ -298,7 +301,8 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     constexpr int NKC = HD / 32;                     // K loads per block (hd chunks)
     constexpr int VSW = v_stride(DW);
     __shared__ __attribute__((aligned(16))) f16 vt[4][BLK * VSW];
-    __shared__ float red[2][2][4][16];               // [parity][max, sum][key tile][slot]
+    __shared__ float red[2][4][16];                  // [parity][key tile][slot]: tile maxes
+    __shared__ float reds[2][4][64];                 // [parity][key tile][lane]: lane sums
     __shared__ __attribute__((aligned(8))) half4 pt[2][4][4][16];  // [parity][key tile][g][slot]
     __shared__ __attribute__((aligned(16))) half8 qs[NKC][64];     // Q^T operands by lane
     __shared__ uint32_t tail[64];
@@ -416,13 +420,13 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 #pragma unroll
         for (int i = 0; i < 4; i++) tm = fmaxf(tm, x[i]);
         tm = tile_max(tm);
-        if (g == 0) red[par][0][w][n] = tm;
+        if (g == 0) red[par][w][n] = tm;
         if (pv) {
 #pragma unroll
             for (int i = 0; i < NVL; i++) v_store<VSW>(vt[w], i * KPI + lane / LPK, 8 * (lane % LPK), vr[i].get());
         }
         __syncthreads();
-        const float mx = fmaxf(fmaxf(red[par][0][0][n], red[par][0][1][n]), fmaxf(red[par][0][2][n], red[par][0][3][n]));
+        const float mx = fmaxf(fmaxf(red[par][0][n], red[par][1][n]), fmaxf(red[par][2][n], red[par][3][n]));
         const float mn = fmaxf(cs.m, mx);
         const float ms = (mn == -INFINITY) ? 0.0f : mn;
         const float corr = exp2_hw(cs.m - ms);
@@ -434,13 +438,15 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
             ts = ts + (float)e;
             ph[i] = e;
         }
-        ts = tile_sum(ts);
-        if (g == 0) red[par][1][w][n] = ts;
+        reds[par][w][lane] = ts;
         pt[par][w][g][n] = ph;
         __syncthreads();
-        float ps = 0.0f;
+        // The block sum in the multi-row order: per lane the tiles in order, then across
+        // lanes.
+        float ls = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) ps = ps + red[par][1][t][n];
+        for (int t = 0; t < 4; t++) ls = ls + reds[par][t][lane];
+        const float ps = tile_sum(ls);
         cs.l = cs.l * corr + ps;
         cs.m = mn;
         if (pv) {
