@@ -78,8 +78,8 @@ __device__ __forceinline__ void fold(State<NDT>& R, const State<NDT>& c) {
 // The two lane-group crossings of a 16-key tile: permlane swaps hand each lane the pair
 // (x[l], x[l^16]) (or l^32) from the lower and the upper lane, in that order on both lanes,
 // so a max or a sum of the pair is the same bits on both. A slot's sum over a 64-entry block
-// is, per lane, each tile's four keys in order and the four tiles in order, then the pairs
-// across l^16, then across l^32.
+// is, per lane, a chain of dot2 steps over its f16 P values (pairs of keys, the four tiles
+// in order), then the pairs across l^16, then across l^32.
 __device__ __forceinline__ float xmax16(float x) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -97,6 +97,11 @@ __device__ __forceinline__ float xsum32(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 __device__ __forceinline__ float tile_sum(float s) { return xsum32(xsum16(s)); }
+
+// acc + h[0] + h[1] as one dot2 step with (1, 1): exact f16 products, one f32 accumulate.
+__device__ __forceinline__ float pair_sum(half2 h, float acc) {
+    return __builtin_amdgcn_fdot2(h, half2{(f16)1.0f, (f16)1.0f}, acc, false);
+}
 __device__ __forceinline__ float tile_max(float m) { return xmax32(xmax16(m)); }
 
 // O <- O * corr for a wave's slots, skipped when every slot's max held (corr == 1 exactly,
@@ -193,19 +198,19 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
         float mn = fmaxf(s[t].m, mx);
         float ms = (mn == -INFINITY) ? 0.0f : mn;
         float corr = exp2_hw(s[t].m - ms);
-        // The block sum: per lane, each tile's four entries in order, the tiles in order;
-        // then across lanes (l^16, then l^32).
+        // P in f16, and the block sum of those f16 values: per lane a chain of dot2 steps
+        // over the pairs (keys 4g+0,1 and 4g+2,3 of each tile, tiles in order), then across
+        // lanes (l^16, then l^32).
         float ls = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
-            float ts = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                f16 ph = (f16)exp2_hw(x[kt][i] - ms);
-                ts = ts + (float)ph;
-                pb[t][kt >> 1][(kt & 1) * 4 + i] = ph;
+            for (int j = 0; j < 2; j++) {
+                const half2 hp = half2{(f16)exp2_hw(x[kt][2 * j] - ms), (f16)exp2_hw(x[kt][2 * j + 1] - ms)};
+                ls = pair_sum(hp, ls);
+                pb[t][kt >> 1][(kt & 1) * 4 + 2 * j] = hp[0];
+                pb[t][kt >> 1][(kt & 1) * 4 + 2 * j + 1] = hp[1];
             }
-            ls = ls + ts;
         }
         const float ps = tile_sum(ls);
         s[t].l = s[t].l * corr + ps;
@@ -302,7 +307,6 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     constexpr int VSW = v_stride(DW);
     __shared__ __attribute__((aligned(16))) f16 vt[4][BLK * VSW];
     __shared__ float red[2][4][16];                  // [parity][key tile][slot]: tile maxes
-    __shared__ float reds[2][4][64];                 // [parity][key tile][lane]: lane sums
     __shared__ __attribute__((aligned(8))) half4 pt[2][4][4][16];  // [parity][key tile][g][slot]
     __shared__ __attribute__((aligned(16))) half8 qs[NKC][64];     // Q^T operands by lane
     __shared__ uint32_t tail[64];
@@ -431,21 +435,19 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
         const float ms = (mn == -INFINITY) ? 0.0f : mn;
         const float corr = exp2_hw(cs.m - ms);
         half4 ph;
-        float ts = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const f16 e = (f16)exp2_hw(x[i] - ms);
-            ts = ts + (float)e;
-            ph[i] = e;
-        }
-        reds[par][w][lane] = ts;
+        for (int i = 0; i < 4; i++) ph[i] = (f16)exp2_hw(x[i] - ms);
         pt[par][w][g][n] = ph;
         __syncthreads();
-        // The block sum in the multi-row order: per lane the tiles in order, then across
-        // lanes.
+        // The block sum in the multi-row order: per lane the dot2 chain over the four tiles'
+        // pairs in order (every wave reads all four tiles of its lane), then across lanes.
         float ls = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) ls = ls + reds[par][t][lane];
+        for (int t = 0; t < 4; t++) {
+            const half4 h4 = pt[par][t][g][n];
+            ls = pair_sum(half2{h4[0], h4[1]}, ls);
+            ls = pair_sum(half2{h4[2], h4[3]}, ls);
+        }
         const float ps = tile_sum(ls);
         cs.l = cs.l * corr + ps;
         cs.m = mn;

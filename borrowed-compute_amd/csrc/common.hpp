@@ -10,6 +10,7 @@ namespace bchip {
 typedef _Float16 f16;
 typedef f16 half8 __attribute__((ext_vector_type(8)));
 typedef f16 half4 __attribute__((ext_vector_type(4)));
+typedef f16 half2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // List entries (visible KV slots) per attention block: four 16-key MFMA tiles.
