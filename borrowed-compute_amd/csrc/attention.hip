@@ -974,7 +974,43 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0xF70);
 }
 
-template <int W, int NT>
+// V^T tiles of a prefill call (written by vt_pack): per KV head, hd rows of npad keys, each
+// 32-key group stored in the order the PV operand takes it (lane group g holds keys
+// 4g..4g+3 and 16+4g..16+4g+3), so that a lane's eight keys of one dim are 16 contiguous
+// bytes: V^T operands are plain 16-byte LDS reads instead of transposing ones.
+__device__ __forceinline__ uint32_t vt_pos(uint32_t q) {  // key q of a 32-group -> position
+    return 8 * ((q & 15) >> 2) + 4 * (q >> 4) + (q & 3);
+}
+
+__global__ __launch_bounds__(256) void vt_pack(const f16* __restrict__ vc, f16* __restrict__ vt, uint32_t kvd,
+                                               uint32_t nkeys, uint32_t npad) {
+    constexpr int HD = 128, TS = HD + 2;
+    __shared__ f16 tile[64 * TS];
+    const uint32_t kvh = blockIdx.y, key0 = blockIdx.x * 64, tid = threadIdx.x;
+    // 64 keys x 128 dims in, rows past the list as zeros.
+    for (uint32_t e = tid; e < 64 * (HD / 8); e += 256) {
+        const uint32_t r = e / (HD / 8), c = 8 * (e % (HD / 8)), key = key0 + r;
+        half8 v = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (key < nkeys) v = *(const half8*)(vc + (size_t)key * kvd + (size_t)kvh * HD + c);
+#pragma unroll
+        for (int j = 0; j < 8; j++) tile[r * TS + c + j] = v[j];
+    }
+    __syncthreads();
+    // hd rows of 64 positions out: 8 positions (16 bytes) a thread per step.
+    for (uint32_t e = tid; e < HD * 8; e += 256) {
+        const uint32_t d = e / 8, p0 = 8 * (e % 8);
+        half8 v;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t pos = p0 + j, b = pos / 32, pq = pos % 32;
+            const uint32_t q = 4 * (pq / 8) + 16 * ((pq % 8) / 4) + (pq % 4);  // inverse of vt_pos
+            v[j] = tile[(32 * b + q) * TS + d];
+        }
+        *(half8*)(vt + ((size_t)kvh * HD + d) * npad + key0 + p0) = v;
+    }
+}
+
+template <int W, int NT, bool VT>
 __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     constexpr int HD = 128;
     constexpr int SL = W * NT * 16;
@@ -1014,6 +1050,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
 
     const f16* kcb = (const f16*)p.kc + (size_t)kvh * hd;
     const f16* vcb = (const f16*)p.vc + (size_t)kvh * hd;
+    const f16* vtb = (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad;
     uint32_t kb0, kb1;
     if (p.split) {
         kb0 = cs_idx * CHUNK_MULTI;
@@ -1033,9 +1070,19 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
             const uint32_t key = key0 + row;
             const bool ok = key < kb1;
             const f16* ks = ok ? kcb + (size_t)key * kvd + 8 * (pch ^ pf_kswz(row)) : zp + 8 * pch;
-            const f16* vs = ok ? vcb + (size_t)key * kvd + 8 * (pch ^ pf_vswz(row)) : zp + 8 * pch;
             __builtin_amdgcn_global_load_lds((const void*)ks, (__attribute__((address_space(3))) void*)&kl[st][q * RPI * HD], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)&vl[st][q * RPI * HD], 16, 0, 0);
+            if constexpr (VT) {
+                // V^T rows (dims) of 64 keys = 128 bytes: 8 dim rows an instruction, chunk
+                // (l % 8) ^ (dim % 8) of dim row q * 8 + l / 8 (keys past the list are zero
+                // in the packed copy, which ends at the last block: the prefetch past the
+                // last block reads the zero page).
+                const uint32_t d = q * 8 + lane / 8, vch = (lane % 8) ^ (d % 8);
+                const f16* vs = key0 < kb1 ? vtb + (size_t)d * p.vt_npad + key0 + 8 * vch : zp + 8 * (lane % 8);
+                __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)&vl[st][q * 8 * BLK], 16, 0, 0);
+            } else {
+                const f16* vs = ok ? vcb + (size_t)key * kvd + 8 * (pch ^ pf_vswz(row)) : zp + 8 * pch;
+                __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)&vl[st][q * RPI * HD], 16, 0, 0);
+            }
         }
     };
 
@@ -1070,13 +1117,19 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
                 return *(const half8*)&kls[r * HD + 8 * (ch ^ pf_kswz(r))];
             },
             [&](int dt, int kc) {
-                // transposing read: source lane j of its 16-lane group names row
-                // kbase + j/4, dims 16dt + 4(j%4): chunk 2dt + (j%4)/2, half (j%4)%2
-                const uint32_t r = 32 * kc + 4 * g + (n >> 2), ch = 2 * dt + ((n & 3) >> 1), h = n & 1;
-                const half4 a = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
-                const uint32_t r2 = r + 16;
-                const half4 b = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
-                return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                if constexpr (VT) {
+                    // dim row 16dt + n, the 8 keys of lane group g in key half kc
+                    const uint32_t d = 16 * dt + n, ch = (4 * kc + g) ^ (d % 8);
+                    return *(const half8*)&vls[d * BLK + 8 * ch];
+                } else {
+                    // transposing read: source lane j of its 16-lane group names row
+                    // kbase + j/4, dims 16dt + 4(j%4): chunk 2dt + (j%4)/2, half (j%4)%2
+                    const uint32_t r = 32 * kc + 4 * g + (n >> 2), ch = 2 * dt + ((n & 3) >> 1), h = n & 1;
+                    const half4 a = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
+                    const uint32_t r2 = r + 16;
+                    const half4 b = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
+                    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                }
             },
             key0, len);
         st ^= 1;
@@ -1275,10 +1328,25 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     const uint32_t blocks = groups * (sp.split ? sp.nchunk : 1u);
     hipError_t e;
     if (a.kv_type == 1 && a.hd == 128) {
-        if (wide)
-            hipLaunchKernelGGL((attn_prefill<8, 1>), dim3(blocks), dim3(512), 0, s, sp);
-        else
-            hipLaunchKernelGGL((attn_prefill<4, 1>), dim3(blocks), dim3(256), 0, s, sp);
+        // Many rows re-read every V block many times: transpose V once (a pass over V) so
+        // that its operands are plain LDS reads. The result is the same bits either way.
+        const bool use_vt = wide && !sp.split && a.rows >= 256;
+        if (use_vt) {
+            const uint32_t nb = ceil_div(maxlen, 64);
+            sp.vt_npad = nb * 64;
+            e = ws.reserve_vt((size_t)a.nkv * 128 * sp.vt_npad * 2);
+            if (e != hipSuccess) return e;
+            sp.vt = ws.vt;
+            hipLaunchKernelGGL(vt_pack, dim3(nb, a.nkv), dim3(256), 0, s, (const f16*)a.vc,
+                               (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, sp.vt_npad);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((attn_prefill<8, 1, true>), dim3(blocks), dim3(512), 0, s, sp);
+        } else if (wide) {
+            hipLaunchKernelGGL((attn_prefill<8, 1, false>), dim3(blocks), dim3(512), 0, s, sp);
+        } else {
+            hipLaunchKernelGGL((attn_prefill<4, 1, false>), dim3(blocks), dim3(256), 0, s, sp);
+        }
         e = hipGetLastError();
     } else if (a.kv_type == 1) {
         if (wide) {

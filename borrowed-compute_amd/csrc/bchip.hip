@@ -130,6 +130,17 @@ hipError_t Workspace::reserve(size_t need_slots, size_t hd_pad) {
     return hipSuccess;
 }
 
+hipError_t Workspace::reserve_vt(size_t bytes) {
+    if (bytes <= vt_bytes && vt) return hipSuccess;
+    if (vt) (void)hipFree(vt);
+    vt = nullptr;
+    vt_bytes = 0;
+    hipError_t e = hipMalloc(&vt, bytes);
+    if (e != hipSuccess) return e;
+    vt_bytes = bytes;
+    return hipSuccess;
+}
+
 hipError_t Workspace::init() {
     hipError_t e = hipMalloc(&zero, ZERO_BYTES);
     if (e != hipSuccess) return e;
@@ -139,7 +150,10 @@ hipError_t Workspace::init() {
 void Workspace::release() {
     if (o) (void)hipFree(o);
     if (ml) (void)hipFree(ml);
+    if (vt) (void)hipFree(vt);
     o = ml = nullptr;
+    vt = nullptr;
+    vt_bytes = 0;
     slots = hdp = 0;
 }
 

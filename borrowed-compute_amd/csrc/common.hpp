@@ -79,6 +79,8 @@ struct SharedParams {
     uint32_t rows, nh, nkv, hd, G;
     uint32_t pos;   // slot of row 0
     float sc;
+    const void* vt;    // V^T tiles (prefill kernel), vt_npad keys a dim row
+    uint32_t vt_npad;
     uint32_t rb;    // rows per workgroup
     uint32_t nrb;   // row blocks
     uint32_t nchunk;// chunks of the longest list (split launches)

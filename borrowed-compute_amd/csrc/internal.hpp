@@ -14,9 +14,11 @@ struct Workspace {
     float* o = nullptr;    // [units*slots][hd_pad]: chunk states
     float* ml = nullptr;   // [units*slots][2]
     void* zero = nullptr;  // ZERO_BYTES of zeros
-    size_t slots = 0, hdp = 0;
+    void* vt = nullptr;    // V^T tiles of a prefill call
+    size_t slots = 0, hdp = 0, vt_bytes = 0;
     hipError_t init();     // allocates the zero page
     hipError_t reserve(size_t need_slots, size_t hd_pad);
+    hipError_t reserve_vt(size_t bytes);
     void release();
 };
 
