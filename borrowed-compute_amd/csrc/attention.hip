@@ -237,6 +237,8 @@ template <>
 struct Raw<f16> {
     half8 v;
     __device__ __forceinline__ void load(const f16* p) { v = *(const half8*)p; }
+    // A load marked as streaming (read once: kept out of the caches' reuse).
+    __device__ __forceinline__ void load_stream(const f16* p) { v = __builtin_nontemporal_load((const half8*)p); }
     __device__ __forceinline__ half8 get() const { return v; }
 };
 template <>
@@ -245,6 +247,11 @@ struct Raw<float> {
     __device__ __forceinline__ void load(const float* p) {
         a = *(const float4*)p;
         b = *(const float4*)(p + 4);
+    }
+    __device__ __forceinline__ void load_stream(const float* p) {
+        const f32x4 x = __builtin_nontemporal_load((const f32x4*)p), y = __builtin_nontemporal_load((const f32x4*)(p + 4));
+        a = float4{x[0], x[1], x[2], x[3]};
+        b = float4{y[0], y[1], y[2], y[3]};
     }
     __device__ __forceinline__ half8 get() const {
         return half8{(f16)a.x, (f16)a.y, (f16)a.z, (f16)a.w, (f16)b.x, (f16)b.y, (f16)b.z, (f16)b.w};
@@ -282,8 +289,8 @@ __device__ __forceinline__ uint32_t nth_set_bit(uint32_t lo, uint32_t hi, uint32
 // ---------------------------------------------------------------------------------------
 // Decode kernel: the G query heads of one row against one KV head for one chunk of the
 // row's list, four waves splitting every block. It writes the chunk's softmax state
-// (m, l, O), or, for a row of one chunk, the normalised output; attn_decode_fold (one-row
-// passes) or attn_combine (multi-row tree passes) combines the chunk states.
+// (m, l, O), or, for a row of one chunk, the normalised output; attn_combine folds the
+// chunk states of multi-row passes (tree rows, a few line rows) left to right.
 template <int NDT>
 __device__ __forceinline__ void store_state(const State<NDT>& st, float* o_row, float* ml, uint32_t d0, uint32_t hd,
                                             int g, bool write_ml) {
@@ -498,14 +505,22 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 // ---------------------------------------------------------------------------------------
 // One-row kernel (decode steps and ragged batches of them). A one-row list is bound only to
 // be deterministic and within rounding of the same row in a batch, so it need not share the
-// multi-row arithmetic: each wave streams one (chunk, KV head) unit alone, in blocks of 32
+// multi-row arithmetic: each wave streams one (chunk, KV head) unit alone, in blocks of RB
 // entries, with no barrier and no exchange between waves. Lane (n, g) holds slot n (query
-// head kvh * G + n) of keys 4g..4g+3 of each 16-key tile; the block's max and sum cross
-// the four lane groups by permlane swaps, which hand every lane the pair (x[l], x[l^16]) or
+// head kvh * G + n) of keys 4g..4g+3 of each 16-key tile; the block's max and sum cross the
+// four lane groups by permlane swaps, which hand every lane the pair (x[l], x[l^16]) or
 // (x[l], x[l^32]) in the same order. V goes through the wave's own LDS rows and comes back
-// transposed. The four waves of a workgroup take consecutive units: four KV heads of one
-// chunk, so a workgroup reads whole stretches of cache rows together.
-constexpr int RB = 32;  // list entries per block of the one-row kernel
+// transposed. The four waves of a workgroup take consecutive units, four KV heads of one
+// chunk, so a workgroup reads 4 * hd contiguous elements of every row it streams (measured
+// faster than four chunks of one head: 25.5 against 30.9 us at 32768 slots x 8 KV heads).
+// A unit whose chunk is the whole list writes the output; otherwise its state goes to the
+// workspace and attn_row_fold combines a row's chunks. (Folding in the last workgroup to
+// finish, found by an arrival counter, would save that launch, but publishing each state
+// takes a device-scope release, an L2 write-back per workgroup: measured at +8 us for 256
+// workgroups and +175 us for 4096 on MI355X.)
+constexpr int RB = 32;                     // list entries per block of the one-row kernel
+constexpr uint32_t ROW_MAX_CHUNKS = 256;   // chunks per (item, KV head): attn_row_fold's reach
+constexpr uint32_t ROW_FOLD_BATCH = 16;    // chunk states a thread loads before folding them
 
 template <int HD, typename KVT>
 __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) {
@@ -523,10 +538,10 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     uint32_t it = 0;
     while (it + 1 < p.nitems && u >= p.items[it + 1].unit0) it++;
     const Item I = p.items[it];
-    const uint32_t hd = p.hd, kvd = p.nkv * hd;
+    const uint32_t hd = p.hd, kvd = p.nkv * hd, G = p.G;
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = rem % p.nkv;
-    const uint32_t len = I.len, kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, len);
-    const bool valid = (uint32_t)n < p.G;
+    const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, I.len);
+    const bool valid = (uint32_t)n < G;
     const KVT* zp = (const KVT*)p.zero;
     const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
     const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
@@ -534,7 +549,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     // Q^T operands (B of the score MFMAs), straight into registers.
     half8 qb[NKC];
     {
-        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * p.G + (valid ? n : 0)) * hd;
+        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * G + (valid ? n : 0)) * hd;
         float4 qa[NKC], qc[NKC];
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++) {
@@ -544,9 +559,10 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
             qc[c2] = *(const float4*)(src + 4);
         }
 #pragma unroll
-        for (int c2 = 0; c2 < NKC; c2++)
-            qb[c2] = q_scaled(qa[c2], qc[c2], p.sc);
+        for (int c2 = 0; c2 < NKC; c2++) qb[c2] = q_scaled(qa[c2], qc[c2], p.sc);
     }
+    // Block key0 into registers; entries at or past kb1 read the zero page (no HBM traffic,
+    // no branch between the loads).
     auto load_block = [&](uint32_t key0, Raw<KVT> (&kr)[2][NKC], Raw<KVT> (&vr)[NVL]) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -555,14 +571,14 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
 #pragma unroll
             for (int c2 = 0; c2 < NKC; c2++) {
                 const uint32_t hd0 = 32 * c2 + 8 * g;
-                kr[t][c2].load((key < kb1 && hd0 < hd) ? row + hd0 : zp);
+                kr[t][c2].load_stream((key < kb1 && hd0 < hd) ? row + hd0 : zp);
             }
         }
         const uint32_t d = 8 * (lane % VLR);
 #pragma unroll
         for (int i = 0; i < NVL; i++) {
             const uint32_t key = key0 + i * VRI + lane / VLR;
-            vr[i].load((key < kb1 && d < hd) ? vc + (size_t)key * kvd + d : zp);
+            vr[i].load_stream((key < kb1 && d < hd) ? vc + (size_t)key * kvd + d : zp);
         }
     };
     f32x4 o[NDT];
@@ -611,8 +627,8 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         for (int dt = 0; dt < NDT; dt++) o[dt] = mfma16(v_operand<VS>(vw, dt, 0, g, n), pb, o[dt]);
     };
     // Two register sets in turn where they fit (f16, hd <= 128): the next block loads while
-    // this one computes. Wider rows load and compute one block at a time; their eight
-    // resident waves per CU still overlap one another.
+    // this one computes. Wider rows load and compute one block at a time; the other resident
+    // waves of the CU still overlap them.
     if constexpr (sizeof(KVT) == 2 && HD <= 128) {
         Raw<KVT> kA[2][NKC], vA[NVL], kB[2][NKC], vB[NVL];
         load_block(kb0, kA, vA);
@@ -628,23 +644,23 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         }
     } else {
         Raw<KVT> kA[2][NKC], vA[NVL];
-        for (uint32_t key0 = kb0;;) {
+        for (uint32_t key0 = kb0; key0 < kb1; key0 += RB) {
             load_block(key0, kA, vA);
             compute_block(key0, kA, vA);
-            key0 += RB;
-            if (key0 >= kb1) break;
         }
     }
     if (!valid) return;
     if (I.nchunk == 1) {
-        float* orow = p.out + ((size_t)I.row * p.nh + kvh * p.G + n) * hd;
+        float* orow = p.out + ((size_t)I.row * p.nh + kvh * G + n) * hd;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             const uint32_t d = 16 * dt + 4 * g;
             if (d < hd) *(float4*)(orow + d) = float4{o[dt][0] / l, o[dt][1] / l, o[dt][2] / l, o[dt][3] / l};
         }
     } else {
-        const size_t at = (size_t)u * 16 + n;  // u is the canonical unit0 + c * nkv + kvh
+        // State at the canonical index of (item, KV head, chunk): a group's chunks are
+        // contiguous for the fold.
+        const size_t at = ((size_t)I.unit0 + (size_t)kvh * I.nchunk + c) * 16 + n;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             const uint32_t d = 16 * dt + 4 * g;
@@ -654,101 +670,65 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     }
 }
 
-// The combination of a one-row list's chunk states, for one (item, KV head, slot): with
-// M = the largest chunk max (exact in any order) and w_c = 2^(m_c - M), O = sum_c w_c o_c
-// and L = sum_c w_c l_c, each summed by a perfect binary tree over the chunk index padded
-// to a power of two with zeros (a zero adds exactly, so the padding width does not change
-// the sums), and out = O / L. The tree is fixed by the chunk count alone.
-// A workgroup takes FOLD_DIMS dims of one slot: thread (cl, dg) holds the aligned run of R
-// chunks cl*R .. cl*R+R-1 (32 runs) for dims 4dg .. 4dg+3, sums it as a subtree in
-// registers, then the runs pair up across lanes (cl^1, cl^2, cl^4: lane bits 3-5) and
-// across the four waves in LDS. Every load is issued before the first use.
-constexpr int FOLD_DIMS = 32;
-constexpr int FOLD_RUNS = 32;
-
+// The fold of a one-row list's chunk states, for one (item, KV head, slot) per workgroup:
+// R thread subsets each fold a contiguous range of chunks from a cleared state, in chunk
+// order (loads of ROW_FOLD_BATCH states issued before the first use), then the R subset
+// states are folded in subset order and normalised. The order is fixed by the chunk count
+// and the shape alone.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_decode_fold(const DirectParams p) {
-    __shared__ float wmax[4];
-    __shared__ float4 wo[4][8];
-    __shared__ float wl[4];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint32_t dg = tid & 7, cl = tid >> 3;
-    const uint32_t hd = p.hd, nslice = (hd + FOLD_DIMS - 1) / FOLD_DIMS;
-    // Workgroup -> (item, KV head, slot, dim slice) over the items with more than one chunk.
-    uint32_t b = blockIdx.x, it = 0;
-    for (;; it++) {
-        const uint32_t here = p.items[it].nchunk > 1 ? p.nkv * p.G * nslice : 0u;
-        if (b < here || it + 1 >= p.nitems) break;
-        b -= here;
-    }
-    const Item I = p.items[it];
-    const uint32_t slice = b % nslice, kvh = (b / nslice) / p.G, slot = (b / nslice) % p.G;
-    const uint32_t nch = I.nchunk, d = slice * FOLD_DIMS + 4 * dg;
-    const bool dok = d < hd;
-    uint32_t N = FOLD_RUNS;
-    while (N < nch) N <<= 1;
-    const uint32_t R = N / FOLD_RUNS;
-    // Leaves of this thread's run, loaded together; chunks past nch are zero leaves.
-    constexpr int RMAX = 8;
-    float2 ml[RMAX];
-    float4 o[RMAX];
+__global__ __launch_bounds__(256) void attn_row_fold(const DirectParams p) {
+    constexpr uint32_t D4 = HD / 4;      // threads per subset: 4 dims each
+    constexpr uint32_t R = 256 / D4;     // subsets
+    __shared__ float4 rO[R][D4];
+    __shared__ float2 rML[R][D4];
+    const uint32_t b = blockIdx.x, per_item = p.nkv * p.G;
+    const Item I = p.items[b / per_item];
+    const uint32_t nch = I.nchunk;
+    if (nch <= 1) return;  // written by the decode kernel
+    const uint32_t kvh = (b % per_item) / p.G, s = (b % per_item) % p.G;
+    const uint32_t tid = threadIdx.x, r = tid / D4, d = 4 * (tid % D4);
+    const uint32_t c0 = r * nch / R, c1 = (r + 1) * nch / R;
+    const size_t cu0 = (size_t)I.unit0 + (size_t)kvh * nch;
+    float M = -INFINITY, L = 0.0f;
+    float4 O = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t cb = c0; cb < c1; cb += ROW_FOLD_BATCH) {
+        float2 ml[ROW_FOLD_BATCH];
+        float4 ov[ROW_FOLD_BATCH];
 #pragma unroll
-    for (int j = 0; j < RMAX; j++) {
-        const uint32_t c = cl * R + j;
-        const bool live = (uint32_t)j < R && c < nch;
-        const size_t at = ((size_t)I.unit0 + (size_t)(live ? c : 0u) * p.nkv + kvh) * 16 + slot;
-        ml[j] = live ? *(const float2*)(p.part_ml + at * 2) : float2{-INFINITY, 0.0f};
-        o[j] = (live && dok) ? *(const float4*)(p.part_o + at * HD + d) : float4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    float mx = -INFINITY;
+        for (uint32_t q = 0; q < ROW_FOLD_BATCH; q++) {
+            const size_t at = (cu0 + min(cb + q, c1 - 1)) * 16 + s;
+            ml[q] = *(const float2*)(p.part_ml + at * 2);
+            ov[q] = *(const float4*)(p.part_o + at * HD + d);
+        }
 #pragma unroll
-    for (int j = 0; j < RMAX; j++) mx = fmaxf(mx, ml[j].x);
-    mx = fmaxf(mx, __shfl_xor(mx, 8));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if (lane == 0) wmax[w] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    const float Ms = M == -INFINITY ? 0.0f : M;
-    // Leaf values, then the run's subtree (R is a power of two <= RMAX; unused leaves are 0
-    // and sit past the run, so the pairing below is the subtree's).
-    float4 vo[RMAX];
-    float vl[RMAX];
-#pragma unroll
-    for (int j = 0; j < RMAX; j++) {
-        const float wc = exp2_hw(ml[j].x - Ms);
-        vo[j] = float4{o[j].x * wc, o[j].y * wc, o[j].z * wc, o[j].w * wc};
-        vl[j] = ml[j].y * wc;
-    }
-#pragma unroll
-    for (int width = RMAX; width > 1; width >>= 1)
-#pragma unroll
-        for (int j = 0; j < width / 2; j++) {
-            if ((uint32_t)width <= R) {
-                vo[j] = float4{vo[2 * j].x + vo[2 * j + 1].x, vo[2 * j].y + vo[2 * j + 1].y,
-                               vo[2 * j].z + vo[2 * j + 1].z, vo[2 * j].w + vo[2 * j + 1].w};
-                vl[j] = vl[2 * j] + vl[2 * j + 1];
+        for (uint32_t q = 0; q < ROW_FOLD_BATCH; q++) {
+            if (cb + q < c1) {
+                float a, bb, mn;
+                merge_coef(M, ml[q].x, a, bb, mn);
+                L = L * a + ml[q].y * bb;
+                O = float4{O.x * a + ov[q].x * bb, O.y * a + ov[q].y * bb, O.z * a + ov[q].z * bb, O.w * a + ov[q].w * bb};
+                M = mn;
             }
         }
-    float4 so = vo[0];
-    float sl = vl[0];
-#pragma unroll
-    for (int x = 8; x <= 32; x <<= 1) {
-        so = float4{so.x + __shfl_xor(so.x, x), so.y + __shfl_xor(so.y, x), so.z + __shfl_xor(so.z, x),
-                    so.w + __shfl_xor(so.w, x)};
-        sl = sl + __shfl_xor(sl, x);
     }
-    if (lane < 8) wo[w][lane] = so;
-    if (lane == 0) wl[w] = sl;
+    rO[r][tid % D4] = O;
+    rML[r][tid % D4] = float2{M, L};
     __syncthreads();
-    if (tid < 8 && dok) {
-        const float4 a = wo[0][tid], b2 = wo[1][tid], c = wo[2][tid], e = wo[3][tid];
-        const float L = (wl[0] + wl[1]) + (wl[2] + wl[3]);
-        const float4 O = float4{(a.x + b2.x) + (c.x + e.x), (a.y + b2.y) + (c.y + e.y), (a.z + b2.z) + (c.z + e.z),
-                                (a.w + b2.w) + (c.w + e.w)};
-        *(float4*)(p.out + ((size_t)I.row * p.nh + kvh * p.G + slot) * hd + d) =
-            float4{O.x / L, O.y / L, O.z / L, O.w / L};
+    if (r != 0) return;
+    float Mf = -INFINITY, Lf = 0.0f;
+    float4 Of = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t rr = 0; rr < R; rr++) {
+        const float2 mlr = rML[rr][tid];
+        const float4 orr = rO[rr][tid];
+        float a, bb, mn;
+        merge_coef(Mf, mlr.x, a, bb, mn);
+        Lf = Lf * a + mlr.y * bb;
+        Of = float4{Of.x * a + orr.x * bb, Of.y * a + orr.y * bb, Of.z * a + orr.z * bb, Of.w * a + orr.w * bb};
+        Mf = mn;
     }
+    if (d < p.hd)
+        *(float4*)(p.out + ((size_t)I.row * p.nh + kvh * p.G + s) * p.hd + d) = float4{Of.x / Lf, Of.y / Lf, Of.z / Lf, Of.w / Lf};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1169,23 +1149,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
 
 static uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
-// Chunk of a one-row list with nkv KV heads: the smallest multiple of the one-row kernel's
-// block (at least two blocks) that cuts the list into at most 1024 / nkv chunks (at least
-// 1, at most 8 * FOLD_RUNS = 256, what attn_decode_fold takes). A long step then has about
-// 1024 wave units, four per CU, all issuing their loads from the start (measured at 32768
-// slots x 8 KV heads: 512 units 33.2 us, 1024 units 28.6 us, 2048 units 31.2 us per call);
-// a multiple of the block rather than a power of two keeps the count near 1024 for every
-// length. Any u32 list length fits.
-uint32_t decode_chunk(uint64_t len, uint32_t nkv) {
-    uint64_t most = 1024 / (nkv ? nkv : 1);
-    if (most < 1) most = 1;
-    if (most > 8 * FOLD_RUNS) most = 8 * FOLD_RUNS;
-    uint64_t c = (len + most - 1) / most;
-    c = (c + RB - 1) / RB * RB;
-    if (c < 2 * RB) c = 2 * RB;
-    return (uint32_t)c;
-}
-
 template <int HD>
 static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s) {
     cp.ngroups = groups;
@@ -1219,22 +1182,27 @@ template <int HD>
 static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s);
 
 template <int HD, typename KVT>
-static hipError_t launch_decode_t(DirectParams& dp, uint32_t folds, CombineParams* left, hipStream_t s) {
+static hipError_t launch_decode_t(DirectParams& dp, CombineParams& cp, hipStream_t s) {
     const dim3 block(256);
     if (dp.tree)
         hipLaunchKernelGGL((attn_decode<HD, KVT, true>), dim3(dp.nunits), block, 0, s, dp);
-    else if (left)
-        hipLaunchKernelGGL((attn_decode<HD, KVT, false>), dim3(dp.nunits), block, 0, s, dp);
     else
-        hipLaunchKernelGGL((attn_decode_row<HD, KVT>), dim3(ceil_div(dp.nunits, 4)), block, 0, s, dp);
+        hipLaunchKernelGGL((attn_decode<HD, KVT, false>), dim3(dp.nunits), block, 0, s, dp);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || folds == 0) return e;
-    if (left) return launch_combine_t<HD>(*left, dp.nitems * dp.nkv, s);
-    hipLaunchKernelGGL((attn_decode_fold<HD>), dim3(folds), block, 0, s, dp);
+    if (e != hipSuccess) return e;
+    return launch_combine_t<HD>(cp, dp.nitems * dp.nkv, s);
+}
+
+template <int HD, typename KVT>
+static hipError_t launch_row_t(const DirectParams& dp, bool fold, hipStream_t s) {
+    hipLaunchKernelGGL((attn_decode_row<HD, KVT>), dim3(ceil_div(dp.nunits, 4)), dim3(256), 0, s, dp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !fold) return e;
+    hipLaunchKernelGGL((attn_row_fold<HD>), dim3(dp.nitems * dp.nkv * dp.G), dim3(256), 0, s, dp);
     return hipGetLastError();
 }
 
-hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s) {
+static DirectParams direct_params(const AttnCall& a, const Workspace& ws, uint32_t nitems) {
     DirectParams dp{};
     dp.zero = ws.zero;
     dp.q = a.q;
@@ -1251,45 +1219,94 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
     dp.tree = a.tree;
     dp.sc = a.scale * LOG2E;
     dp.nitems = nitems;
-    uint32_t units = 0, folds = 0;
-    const uint32_t nslice = (a.hd + FOLD_DIMS - 1) / FOLD_DIMS;
+    return dp;
+}
+
+// Chunk of a one-row list with nkv KV heads (each (chunk, KV head) is one wave's unit):
+// a multiple of RB (at least two blocks) that cuts the list into at most ROW_UNITS / nkv
+// chunks, and at most ROW_MAX_CHUNKS. A long step then has about ROW_UNITS waves, four per
+// CU, all issuing their loads from the start (measured at 32768 slots x 8 KV heads: 512
+// units 33.2 us, 1024 units 28.6 us, 2048 units 31.2 us per call). It depends only on the
+// list's own length and nkv, so a sequence gets the same bits in any ragged batch as alone.
+constexpr uint64_t ROW_UNITS = 1024;
+
+uint32_t row_chunk(uint64_t len, uint32_t nkv) {
+    uint64_t most = std::max<uint64_t>(1, ROW_UNITS / std::max<uint32_t>(nkv, 1));
+    most = std::min<uint64_t>(most, ROW_MAX_CHUNKS);
+    uint64_t chunk = (len + most - 1) / most;
+    chunk = (chunk + RB - 1) / RB * RB;
+    return (uint32_t)std::max<uint64_t>(chunk, 2 * RB);
+}
+
+hipError_t row_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s) {
+    if (nitems == 0 || nitems > MAX_ITEMS) return hipErrorInvalidValue;
+    DirectParams dp = direct_params(a, ws, nitems);
+    dp.tree = 0;
+    uint64_t units = 0;
+    bool fold = false;
+    for (uint32_t i = 0; i < nitems; i++) {
+        Item& I = dp.items[i];
+        I = items[i];
+        if (I.len == 0) return hipErrorInvalidValue;
+        I.nrows = 1;
+        I.chunk = row_chunk(I.len, a.nkv);
+        I.nchunk = ceil_div(I.len, I.chunk);
+        I.unit0 = (uint32_t)units;
+        units += (uint64_t)a.nkv * I.nchunk;
+        fold = fold || I.nchunk > 1;
+    }
+    if (units > 0x7fffffffull) return hipErrorInvalidValue;
+    dp.nunits = (uint32_t)units;
+    const int hdp = pad_hd(a.hd);
+    hipError_t e = ws.reserve((size_t)units * 16, (size_t)hdp);
+    if (e != hipSuccess) return e;
+    dp.part_o = ws.o;
+    dp.part_ml = ws.ml;
+    if (a.kv_type == 1) {
+        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, f16>(dp, fold, s)));
+    } else {
+        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, float>(dp, fold, s)));
+    }
+    return e;
+}
+
+// Multi-row passes of decode-kernel units (tree rows, a few line rows): chunk states folded
+// left to right by attn_combine, as every multi-row line is, so that a tree row matches its
+// line bit for bit.
+hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s) {
+    if (nitems == 0 || nitems > MAX_ITEMS) return hipErrorInvalidValue;
+    DirectParams dp = direct_params(a, ws, nitems);
+    uint32_t units = 0;
     const int hdp = pad_hd(a.hd);
     for (uint32_t i = 0; i < nitems; i++) {
         Item& I = dp.items[i];
         I = items[i];
         I.unit0 = units;
         units += a.nkv * I.nchunk;
-        if (I.nchunk > 1) folds += a.nkv * dp.G * nslice;
-        if (a.rows == 1 && I.nchunk > 8 * FOLD_RUNS) return hipErrorInvalidValue;  // decode_chunk keeps to 256
     }
     dp.nunits = units;
     hipError_t e = ws.reserve((size_t)units * 16, (size_t)hdp);
     if (e != hipSuccess) return e;
     dp.part_o = ws.o;
     dp.part_ml = ws.ml;
-    // Multi-row tree passes fold chunks left to right, as every multi-row line does, so that
-    // a tree row matches its line bit for bit; one-row passes use the tree combination.
     CombineParams cp{};
-    const bool left = a.rows >= 2;
-    if (left) {
-        cp.zero = ws.zero;
-        cp.out = a.out;
-        cp.part_o = ws.o;
-        cp.part_ml = ws.ml;
-        cp.nh = a.nh;
-        cp.nkv = a.nkv;
-        cp.hd = a.hd;
-        cp.G = dp.G;
-        cp.slots = 16;
-        cp.slots_out = 16;
-        cp.shared = 0;
-        cp.nitems = nitems;
-        for (uint32_t i = 0; i < nitems; i++) cp.items[i] = dp.items[i];
-    }
+    cp.zero = ws.zero;
+    cp.out = a.out;
+    cp.part_o = ws.o;
+    cp.part_ml = ws.ml;
+    cp.nh = a.nh;
+    cp.nkv = a.nkv;
+    cp.hd = a.hd;
+    cp.G = dp.G;
+    cp.slots = 16;
+    cp.slots_out = 16;
+    cp.shared = 0;
+    cp.nitems = nitems;
+    for (uint32_t i = 0; i < nitems; i++) cp.items[i] = dp.items[i];
     if (a.kv_type == 1) {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, f16>(dp, folds, left ? &cp : nullptr, s)));
+        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, f16>(dp, cp, s)));
     } else {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, float>(dp, folds, left ? &cp : nullptr, s)));
+        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, float>(dp, cp, s)));
     }
     return e;
 }

@@ -400,8 +400,14 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     const uint32_t per = std::max(1u, 16u / (nh / nkv));
     const uint32_t nline = (rows + per - 1) / per;
     const bool short_line = !tree && rows >= 2 && nline <= 4;
-    if (rows == 1 || tree || short_line) {
-        const uint32_t chunk = rows == 1 ? decode_chunk(slots, nkv) : CHUNK_MULTI;
+    if (rows == 1 && !tree) {
+        Item item{};
+        item.row = 0;
+        item.nrows = 1;
+        item.len = (uint32_t)slots;
+        e = row_attention(a, &item, 1, c->ws, c->stream);
+    } else if (tree || short_line) {
+        const uint32_t chunk = CHUNK_MULTI;
         Item items[MAX_ITEMS];
         const uint32_t nitems = short_line ? nline : rows;
         for (uint32_t i = 0; i < nitems; i++) {
@@ -449,18 +455,14 @@ int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const v
         const uint32_t ns = std::min<uint32_t>(MAX_ITEMS, nseq - s0);
         Item items[MAX_ITEMS];
         for (uint32_t i = 0; i < ns; i++) {
-            const uint32_t len = seq_lens[s0 + i];
-            const uint32_t chunk = decode_chunk(len, nkv);
             Item& I = items[i];
             I = Item{};
             I.row = s0 + i;
             I.nrows = 1;
-            I.len = len;
-            I.nchunk = (len + chunk - 1) / chunk;
-            I.chunk = chunk;
+            I.len = seq_lens[s0 + i];
             I.kvoff = kv_offsets[s0 + i];
         }
-        HIP_TRY(direct_attention(a, items, ns, c->ws, c->stream), "ragged attention");
+        HIP_TRY(row_attention(a, items, ns, c->ws, c->stream), "ragged attention");
     }
     return BCHIP_OK;
 }

@@ -36,7 +36,9 @@ struct AttnCall {
     uint64_t slot_limit;  // slots both caches hold (all slots a call may read when unknown)
 };
 
-uint32_t decode_chunk(uint64_t len, uint32_t nkv);
+// One-row items (row, len, kvoff): decode steps and ragged batches, one launch.
+hipError_t row_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s);
+// Multi-row items (tree rows, short lines) with chunk and nchunk set.
 hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
                             Workspace& ws, hipStream_t s);
 hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s);
