@@ -32,6 +32,8 @@
 #include "internal.hpp"
 
 #include <math.h>
+#include <type_traits>
+#include <stdlib.h>
 
 namespace bchip {
 
@@ -62,6 +64,22 @@ __device__ __forceinline__ void merge_coef(float M, float m, float& a, float& b,
     float ms = (Mn == -INFINITY) ? 0.0f : Mn;
     a = exp2_hw(M - ms);
     b = exp2_hw(m - ms);
+}
+
+// The running max of a slot moves only when a block's max passes it by more than LAZY
+// (log2 units): until then the block's P = 2^(x - m) may reach 2^LAZY (exact in f16's
+// range) and O and l keep their scale, so most blocks skip the rescale of O. Every kernel
+// applies the same rule per slot, so a row's bits do not depend on which kernel, wave or
+// neighbours computed it. mn: the new max; ms: the subtrahend of the block's exponents (0
+// for a slot that has seen nothing); corr: the factor on O and l (exactly 1 when the max
+// stays, 0 for a slot's first visible block).
+constexpr float LAZY = 8.0f;
+
+__device__ __forceinline__ void lazy_max(float m, float mx, float& mn, float& ms, float& corr) {
+    const bool up = mx > m + LAZY;
+    mn = up ? mx : m;
+    ms = (mn == -INFINITY) ? 0.0f : mn;
+    corr = up ? exp2_hw(m - ms) : 1.0f;
 }
 
 // R <- fold(R, c). attn_combine applies the same per-element expression.
@@ -195,9 +213,8 @@ __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 
 #pragma unroll
             for (int i = 0; i < 4; i++) mx = fmaxf(mx, x[kt][i]);
         mx = tile_max(mx);
-        float mn = fmaxf(s[t].m, mx);
-        float ms = (mn == -INFINITY) ? 0.0f : mn;
-        float corr = exp2_hw(s[t].m - ms);
+        float mn, ms, corr;
+        lazy_max(s[t].m, mx, mn, ms, corr);
         // P in f16, and the block sum of those f16 values: per lane a chain of dot2 steps
         // over the pairs (keys 4g+0,1 and 4g+2,3 of each tile, tiles in order), then across
         // lanes (l^16, then l^32).
@@ -438,9 +455,8 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
         }
         __syncthreads();
         const float mx = fmaxf(fmaxf(red[par][0][n], red[par][1][n]), fmaxf(red[par][2][n], red[par][3][n]));
-        const float mn = fmaxf(cs.m, mx);
-        const float ms = (mn == -INFINITY) ? 0.0f : mn;
-        const float corr = exp2_hw(cs.m - ms);
+        float mn, ms, corr;
+        lazy_max(cs.m, mx, mn, ms, corr);
         half4 ph;
 #pragma unroll
         for (int i = 0; i < 4; i++) ph[i] = (f16)exp2_hw(x[i] - ms);
@@ -606,9 +622,8 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
                 mx = fmaxf(mx, x[t][i]);
             }
         mx = xmax32(xmax16(mx));
-        const float mn = fmaxf(m, mx);
-        const float ms = (mn == -INFINITY) ? 0.0f : mn;
-        const float corr = exp2_hw(m - ms);
+        float mn, ms, corr;
+        lazy_max(m, mx, mn, ms, corr);
         half8 pb;
         float ts = 0.0f;
 #pragma unroll
@@ -990,17 +1005,49 @@ __global__ __launch_bounds__(256) void vt_pack(const f16* __restrict__ vc, f16* 
     }
 }
 
-template <int W, int NT, bool VT>
+// The prefill kernel proper: one 16-slot tile per wave, W waves sharing each K and V block
+// in LDS, block_step's arithmetic. Blocks stream through a ring of STAGES LDS stages (one
+// LDS object each, K then V), fetched STAGES-1 blocks ahead by direct-to-LDS loads, with one
+// barrier per block (measured: a 4-stage ring 465 / 613 TFLOP/s at 2048 / 8192 rows against
+// 411 / 574 with 2 stages). The loop is unrolled by STAGES so that every stage is a
+// compile-time object: the compiler then waits for a stage's own loads before reading it,
+// not for every load in flight. (Computing block b+1's scores beside block b's softmax
+// needs both blocks' scores live at once: past the 256 registers of two waves per SIMD,
+// and the spill reloads then wait for the whole ring: 246 / 308 TFLOP/s.)
+// The per-block work is cut to what the arithmetic needs (the loop is VALU-bound before it
+// is MFMA- or LDS-bound: 8.7 VALU instructions per MFMA in a straightforward build, where
+// about two per MFMA issue alongside the MFMAs for free):
+//  - rows are fetched from per-lane offsets fixed for the whole loop plus a scalar block
+//    base; only a block that ends past the list selects the zero page per lane, and nothing
+//    past the list is fetched;
+//  - LDS operand reads are per-lane bases plus immediate offsets;
+//  - P is rounded to f16 once, for both the block sum and the PV operand.
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+template <int W, bool VT, int STAGES>
 __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     constexpr int HD = 128;
-    constexpr int SL = W * NT * 16;
     constexpr int NKC = HD / 32, NDT = HD / 16;
     constexpr int RPI = 64 / PF_CPR;            // cache rows per load instruction
     constexpr int LPW = BLK / RPI / W;          // load instructions per wave per block (K or V)
-    __shared__ __attribute__((aligned(16))) f16 kl[2][BLK * HD];
-    __shared__ __attribute__((aligned(16))) f16 vl[2][BLK * HD];
+    constexpr int LPB = 2 * LPW;                // K and V loads per wave per block
+    constexpr int SZ = 2 * BLK * HD;            // f16 per stage: K rows, then V (or V^T)
+    static_assert(LPW * RPI * W == BLK, "a block's rows divide over the waves");
+    static_assert(STAGES == 3 || STAGES == 4, "ring of 3 or 4 stages");
+    __shared__ __attribute__((aligned(16))) f16 ring0[SZ];
+    __shared__ __attribute__((aligned(16))) f16 ring1[SZ];
+    __shared__ __attribute__((aligned(16))) f16 ring2[SZ];
+    __shared__ __attribute__((aligned(16))) f16 ring3[STAGES > 3 ? SZ : 8];
+    auto ring = [&](auto S) -> f16* {
+        if constexpr (decltype(S)::value == 0) return ring0;
+        else if constexpr (decltype(S)::value == 1) return ring1;
+        else if constexpr (decltype(S)::value == 2) return ring2;
+        else return ring3;
+    };
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, n = lane & 15;
     const uint32_t gi_launch = p.split ? blockIdx.x / p.nchunk : blockIdx.x;
     const uint32_t cs_idx = p.split ? blockIdx.x % p.nchunk : 0u;
@@ -1010,27 +1057,23 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     const uint32_t r0 = rbi * p.rb;
     const uint32_t rlast = min(r0 + p.rb, p.rows) - 1u;
     const uint32_t maxlen = p.pos + rlast + 1u;
-    const uint32_t hd = p.hd, kvd = p.nkv * hd;
+    const uint32_t kvd = p.nkv * HD;
 
-    half8 qb[NT][NKC];
-    uint32_t len[NT], orow[NT], ohead[NT];
-    bool valid[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const uint32_t sl = (w * NT + t) * 16 + n;
+    // Slot n of this wave is slot 16w + n of the workgroup: head gh, row r0 + rl.
+    half8 qb[NKC];
+    uint32_t len, orow, ohead;
+    bool valid;
+    {
+        const uint32_t sl = 16 * w + n;
         const uint32_t gh = sl / p.rb, rl = sl % p.rb, r = r0 + rl;
-        valid[t] = gh < p.G && r < p.rows;
-        len[t] = valid[t] ? p.pos + r + 1u : 0u;
-        orow[t] = r;
-        ohead[t] = kvh * p.G + gh;
-        const float* qrow = p.q + ((size_t)(valid[t] ? r : 0u) * p.nh + (valid[t] ? ohead[t] : 0u)) * hd;
+        valid = gh < p.G && r < p.rows;
+        len = valid ? p.pos + r + 1u : 0u;
+        orow = r;
+        ohead = kvh * p.G + gh;
+        const float* qrow = p.q + ((size_t)(valid ? r : 0u) * p.nh + (valid ? ohead : 0u)) * HD;
 #pragma unroll
-        for (int c = 0; c < NKC; c++) qb[t][c] = q_operand(qrow, 32 * c + 8 * g, hd, valid[t], p.sc);
+        for (int c = 0; c < NKC; c++) qb[c] = q_operand(qrow, 32 * c + 8 * g, HD, valid, p.sc);
     }
-
-    const f16* kcb = (const f16*)p.kc + (size_t)kvh * hd;
-    const f16* vcb = (const f16*)p.vc + (size_t)kvh * hd;
-    const f16* vtb = (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad;
     uint32_t kb0, kb1;
     if (p.split) {
         kb0 = cs_idx * CHUNK_MULTI;
@@ -1039,108 +1082,214 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         kb0 = 0;
         kb1 = maxlen;
     }
+
+    // Per-lane element offsets of this wave's load instructions, fixed for the loop: K row
+    // 4q + l/16 (q = i*W + w), 16-byte chunk l%16 swizzled by the row; V^T dim row 8q + l/8,
+    // chunk l%8 swizzled by the dim row (VT), else V rows as K.
     const f16* zp = (const f16*)p.zero;
-    // Block key0 into stage st: this wave's LPW instructions for K and for V (rows past kb1
-    // read the zero page).
-    auto load_block = [&](uint32_t key0, int st) {
+    const f16* kcb = (const f16*)p.kc + (size_t)kvh * HD;
+    const f16* vcb = VT ? (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad : (const f16*)p.vc + (size_t)kvh * HD;
+    uint32_t krow[LPW], koff[LPW], voff[LPW];
 #pragma unroll
-        for (int i = 0; i < LPW; i++) {
-            const uint32_t q = i * W + w;                 // instruction of the block
-            const uint32_t row = q * RPI + lane / PF_CPR, pch = lane % PF_CPR;
-            const uint32_t key = key0 + row;
-            const bool ok = key < kb1;
-            const f16* ks = ok ? kcb + (size_t)key * kvd + 8 * (pch ^ pf_kswz(row)) : zp + 8 * pch;
-            __builtin_amdgcn_global_load_lds((const void*)ks, (__attribute__((address_space(3))) void*)&kl[st][q * RPI * HD], 16, 0, 0);
-            if constexpr (VT) {
-                // V^T rows (dims) of 64 keys = 128 bytes: 8 dim rows an instruction, chunk
-                // (l % 8) ^ (dim % 8) of dim row q * 8 + l / 8 (keys past the list are zero
-                // in the packed copy, which ends at the last block: the prefetch past the
-                // last block reads the zero page).
-                const uint32_t d = q * 8 + lane / 8, vch = (lane % 8) ^ (d % 8);
-                const f16* vs = key0 < kb1 ? vtb + (size_t)d * p.vt_npad + key0 + 8 * vch : zp + 8 * (lane % 8);
-                __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)&vl[st][q * 8 * BLK], 16, 0, 0);
-            } else {
-                const f16* vs = ok ? vcb + (size_t)key * kvd + 8 * (pch ^ pf_vswz(row)) : zp + 8 * pch;
-                __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)&vl[st][q * RPI * HD], 16, 0, 0);
+    for (int i = 0; i < LPW; i++) {
+        const uint32_t q = i * W + w, row = q * RPI + lane / PF_CPR, pch = lane % PF_CPR;
+        krow[i] = row;
+        koff[i] = row * kvd + 8 * (pch ^ pf_kswz(row));
+        if constexpr (VT) {
+            const uint32_t d = q * 8 + lane / 8;
+            voff[i] = d * p.vt_npad + 8 * ((lane % 8) ^ (d % 8));
+        } else {
+            voff[i] = row * kvd + 8 * (pch ^ pf_vswz(row));
+        }
+    }
+    typedef __attribute__((address_space(3))) void lds_t;
+    auto load_block = [&](uint32_t key0, auto S) {
+        if (key0 >= kb1) return;  // nothing past the list
+        f16* kl = ring(S);
+        f16* vl = kl + BLK * HD;
+        const f16* kb = kcb + (size_t)key0 * kvd;
+        const f16* vb = VT ? vcb + key0 : vcb + (size_t)key0 * kvd;
+        if (key0 + BLK <= kb1) {
+#pragma unroll
+            for (int i = 0; i < LPW; i++) {
+                const uint32_t q = i * W + w;
+                __builtin_amdgcn_global_load_lds((const void*)(kb + koff[i]), (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(vb + voff[i]), (lds_t*)&vl[q * (VT ? 8 * BLK : RPI * HD)], 16, 0, 0);
+            }
+        } else {
+            // The list's last block: rows past it read the zero page (the packed V^T holds
+            // zeros there already).
+#pragma unroll
+            for (int i = 0; i < LPW; i++) {
+                const uint32_t q = i * W + w;
+                const bool ok = key0 + krow[i] < kb1;
+                const f16* ks = ok ? kb + koff[i] : zp + 8 * (lane % PF_CPR);
+                const f16* vs = (VT || ok) ? vb + voff[i] : zp + 8 * (lane % PF_CPR);
+                __builtin_amdgcn_global_load_lds((const void*)ks, (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)vs, (lds_t*)&vl[q * (VT ? 8 * BLK : RPI * HD)], 16, 0, 0);
             }
         }
     };
-
-    State<NDT> R[NT], cs[NT];
+    // LDS operand bases: K tile kt, hd chunk c at kbase[c] + kt * 16 rows (row 16kt + n has
+    // swizzle n); V^T tile dt, key half kc at vbase[kc] + dt * 16 dim rows (swizzle n % 8).
+    uint32_t kbase[NKC], vbase[2];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        state_clear(R[t]);
-        state_clear(cs[t]);
+    for (int c = 0; c < NKC; c++) kbase[c] = n * HD + 8 * ((4 * c + g) ^ n);
+#pragma unroll
+    for (int kc = 0; kc < 2; kc++) vbase[kc] = n * BLK + 8 * ((4 * kc + g) ^ (n % 8));
+    // S^T = K . Q^T of the block in stage S: four key tiles, hd chunks accumulated in order.
+    auto scores = [&](auto S, f32x4 (&sc4)[4]) {
+        const f16* kls = ring(S);
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            sc4[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < NKC; c++) sc4[kt] = mfma16(*(const half8*)&kls[kbase[c] + kt * 16 * HD], qb[c], sc4[kt]);
+        }
+    };
+    // Barrier without the fence __syncthreads carries: that fence would wait for every
+    // direct-to-LDS load in flight, the later blocks' included. The waits before it are
+    // explicit; LDS reads of a wave finish before its MFMAs consume them, so every read of a
+    // stage is over when its wave reaches the next barrier.
+    auto barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    State<NDT> R, cs;
+    state_clear(R);
+    state_clear(cs);
+    // Prologue: blocks 0 .. STAGES-2 in flight, block 0 in, its scores. (A workgroup of a
+    // split launch may see nothing of its chunk: then it only stores its empty state.)
+    f32x4 scur[4];
+    if (kb0 < kb1) {
+        load_block(kb0, ic<0>{});
+        load_block(kb0 + BLK, ic<1>{});
+        if constexpr (STAGES > 3) load_block(kb0 + 2 * BLK, ic<2>{});
+        // wait for block 0 alone: every later prologue block that was issued may still load
+        if (STAGES > 3 && kb0 + 2 * BLK < kb1)
+            wait_vm<2 * LPB>();
+        else if (kb0 + BLK < kb1)
+            wait_vm<LPB>();
+        else
+            wait_vm<0>();
+        barrier();
     }
-    int st = 0;
-    load_block(kb0, 0);
-    for (uint32_t key0 = kb0; key0 < kb1; key0 += BLK) {
-        // This block's rows are in (own loads: wait; everyone's: barrier); the barrier also
-        // ends every read of the other stage, which the next block's loads then refill.
-        wait_vm<0>();
-        __syncthreads();
-        load_block(key0 + BLK, st ^ 1);
+
+    // One block: S = stage of block b (its V; its K was read one block earlier).
+    auto iter = [&](uint32_t key0, auto S) -> bool {
+        constexpr int s0 = decltype(S)::value;
+        constexpr int sr = (s0 + STAGES - 1) % STAGES;
+        const uint32_t key1 = key0 + BLK;
+        // Block b+1 in (own loads: wait, leaving block b+2's in flight; everyone's: the
+        // barrier), and every read of the stage that block b+STAGES-1 refills is over.
+        if (key1 < kb1) {
+            if (STAGES > 3 && key1 + BLK < kb1)
+                wait_vm<LPB * (STAGES - 3)>();
+            else
+                wait_vm<0>();
+        }
+        barrier();
+        load_block(key0 + (STAGES - 1) * BLK, ic<sr>{});
         if (key0 != kb0 && key0 % CHUNK_MULTI == 0) {
             keep_branch();
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                fold(R[t], cs[t]);
-                state_clear(cs[t]);
-            }
+            fold(R, cs);
+            state_clear(cs);
         }
-        const f16* kls = kl[st];
-        const f16* vls = vl[st];
-        block_step<HD, NT>(
-            cs, qb,
-            [&](int kt, int c) {
-                const uint32_t r = 16 * kt + n, ch = 4 * c + g;
-                return *(const half8*)&kls[r * HD + 8 * (ch ^ pf_kswz(r))];
-            },
-            [&](int dt, int kc) {
+        scores(S, scur);
+        float x[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[kt][i] = scur[kt][i];
+        if (!__all(key0 + BLK <= len)) {
+            keep_branch();
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (key0 + 16 * kt + 4 * g + i >= len) x[kt][i] = -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3]));
+#pragma unroll
+        for (int kt = 1; kt < 4; kt++)
+            mx = fmaxf(mx, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
+        mx = tile_max(mx);
+        float mn, ms, corr;
+        lazy_max(cs.m, mx, mn, ms, corr);
+        // P in f16 once: the block sum (dot2 chain over the pairs, tiles in order, then across
+        // lanes) and the PV operand (keys 32kc + 4g + 0..3, then 32kc + 16 + 4g + 0..3).
+        uint32_t hp[4][2];
+        float ls = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const half2 h = half2{(f16)exp2_hw(x[kt][2 * j] - ms), (f16)exp2_hw(x[kt][2 * j + 1] - ms)};
+                ls = pair_sum(h, ls);
+                hp[kt][j] = __builtin_bit_cast(uint32_t, h);
+            }
+        const float ps = tile_sum(ls);
+        cs.l = cs.l * corr + ps;
+        cs.m = mn;
+        rescale(cs.o, corr);
+        // PV of block b.
+        const f16* vls = ring(S) + BLK * HD;
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++) {
+            const half8 pb = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                half8 a;
                 if constexpr (VT) {
-                    // dim row 16dt + n, the 8 keys of lane group g in key half kc
-                    const uint32_t d = 16 * dt + n, ch = (4 * kc + g) ^ (d % 8);
-                    return *(const half8*)&vls[d * BLK + 8 * ch];
+                    a = *(const half8*)&vls[vbase[kc] + dt * 16 * BLK];
                 } else {
                     // transposing read: source lane j of its 16-lane group names row
                     // kbase + j/4, dims 16dt + 4(j%4): chunk 2dt + (j%4)/2, half (j%4)%2
                     const uint32_t r = 32 * kc + 4 * g + (n >> 2), ch = 2 * dt + ((n & 3) >> 1), h = n & 1;
-                    const half4 a = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
+                    const half4 lo = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
                     const uint32_t r2 = r + 16;
-                    const half4 b = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
-                    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                    const half4 hi = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
+                    a = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 }
-            },
-            key0, len);
-        st ^= 1;
+                cs.o[dt] = mfma16(a, pb, cs.o[dt]);
+            }
+        }
+        return key1 < kb1;
+    };
+    for (uint32_t key0 = kb0; key0 < kb1;) {
+        if (!iter(key0, ic<0>{})) break;
+        key0 += BLK;
+        if (!iter(key0, ic<1>{})) break;
+        key0 += BLK;
+        if (!iter(key0, ic<2>{})) break;
+        key0 += BLK;
+        if constexpr (STAGES > 3) {
+            if (!iter(key0, ic<3 % STAGES>{})) break;
+            key0 += BLK;
+        }
     }
-    wait_vm<0>();  // the prefetch past the end (zero page) lands before the workgroup ends
     if (p.split) {
         const size_t u = (size_t)grp * p.nchunk + cs_idx;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const uint32_t sl = (w * NT + t) * 16 + n;
-            float* po = p.part_o + (u * SL + sl) * HD;
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) {
-                const uint32_t d = 16 * dt + 4 * g;
-                *(float4*)(po + d) = float4{cs[t].o[dt][0], cs[t].o[dt][1], cs[t].o[dt][2], cs[t].o[dt][3]};
-            }
-            if (g == 0) *(float2*)(p.part_ml + (u * SL + sl) * 2) = float2{cs[t].m, cs[t].l};
-        }
-        return;
-    }
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        fold(R[t], cs[t]);
-        if (!valid[t]) continue;
-        float* o = p.out + ((size_t)orow[t] * p.nh + ohead[t]) * hd;
+        const uint32_t sl = 16 * w + n;
+        float* po = p.part_o + (u * (16 * W) + sl) * HD;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             const uint32_t d = 16 * dt + 4 * g;
-            *(float4*)(o + d) = float4{R[t].o[dt][0] / R[t].l, R[t].o[dt][1] / R[t].l, R[t].o[dt][2] / R[t].l,
-                                       R[t].o[dt][3] / R[t].l};
+            *(float4*)(po + d) = float4{cs.o[dt][0], cs.o[dt][1], cs.o[dt][2], cs.o[dt][3]};
         }
+        if (g == 0) *(float2*)(p.part_ml + (u * (16 * W) + sl) * 2) = float2{cs.m, cs.l};
+        return;
+    }
+    fold(R, cs);
+    if (!valid) return;
+    float* o = p.out + ((size_t)orow * p.nh + ohead) * HD;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        const uint32_t d = 16 * dt + 4 * g;
+        *(float4*)(o + d) = float4{R.o[dt][0] / R.l, R.o[dt][1] / R.l, R.o[dt][2] / R.l, R.o[dt][3] / R.l};
     }
 }
 
@@ -1358,11 +1507,11 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
                                (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, sp.vt_npad);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((attn_prefill<8, 1, true>), dim3(blocks), dim3(512), 0, s, sp);
+            hipLaunchKernelGGL((attn_prefill<8, true, 4>), dim3(blocks), dim3(512), 0, s, sp);
         } else if (wide) {
-            hipLaunchKernelGGL((attn_prefill<8, 1, false>), dim3(blocks), dim3(512), 0, s, sp);
+            hipLaunchKernelGGL((attn_prefill<8, false, 4>), dim3(blocks), dim3(512), 0, s, sp);
         } else {
-            hipLaunchKernelGGL((attn_prefill<4, 1, false>), dim3(blocks), dim3(256), 0, s, sp);
+            hipLaunchKernelGGL((attn_prefill<4, false, 4>), dim3(blocks), dim3(256), 0, s, sp);
         }
         e = hipGetLastError();
     } else if (a.kv_type == 1) {
