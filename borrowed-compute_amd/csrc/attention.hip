@@ -1059,8 +1059,11 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     const uint32_t maxlen = p.pos + rlast + 1u;
     const uint32_t kvd = p.nkv * HD;
 
-    // Slot n of this wave is slot 16w + n of the workgroup: head gh, row r0 + rl.
+    // Slot n of this wave is slot 16w + n of the workgroup: head gh, row r0 + rl. Its Q is
+    // loaded here and converted after the first K/V loads are issued, so that the two
+    // latencies overlap.
     half8 qb[NKC];
+    float4 qraw[NKC][2];
     uint32_t len, orow, ohead;
     bool valid;
     {
@@ -1070,9 +1073,13 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         len = valid ? p.pos + r + 1u : 0u;
         orow = r;
         ohead = kvh * p.G + gh;
-        const float* qrow = p.q + ((size_t)(valid ? r : 0u) * p.nh + (valid ? ohead : 0u)) * HD;
+        const float* qrow = valid ? p.q + ((size_t)r * p.nh + ohead) * HD : (const float*)p.zero;
 #pragma unroll
-        for (int c = 0; c < NKC; c++) qb[c] = q_operand(qrow, 32 * c + 8 * g, HD, valid, p.sc);
+        for (int c = 0; c < NKC; c++) {
+            const float* src = valid ? qrow + 32 * c + 8 * g : qrow;
+            qraw[c][0] = *(const float4*)src;
+            qraw[c][1] = *(const float4*)(src + 4);
+        }
     }
     uint32_t kb0, kb1;
     if (p.split) {
@@ -1167,6 +1174,10 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         load_block(kb0, ic<0>{});
         load_block(kb0 + BLK, ic<1>{});
         if constexpr (STAGES > 3) load_block(kb0 + 2 * BLK, ic<2>{});
+    }
+#pragma unroll
+    for (int c = 0; c < NKC; c++) qb[c] = q_scaled(qraw[c][0], qraw[c][1], p.sc);
+    if (kb0 < kb1) {
         // wait for block 0 alone: every later prologue block that was issued may still load
         if (STAGES > 3 && kb0 + 2 * BLK < kb1)
             wait_vm<2 * LPB>();

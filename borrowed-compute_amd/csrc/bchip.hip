@@ -393,35 +393,29 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / row_bytes;
     AttnCall a{q, kc, vc, kv_type, out, masks, tree ? 1u : 0u, rows, nh, nkv, hd, pos, scale, limit};
     hipError_t e;
-    // A few line rows over a long list (speculative verify) run as decode-style units of
-    // 16 / G rows each, split over the list: the shared kernel would have one workgroup per
-    // 256-entry chunk and KV head only. Either kernel computes a row with the same
-    // arithmetic, so the choice does not change a bit of the result.
-    const uint32_t per = std::max(1u, 16u / (nh / nkv));
-    const uint32_t nline = (rows + per - 1) / per;
-    const bool short_line = !tree && rows >= 2 && nline <= 4;
+    // One row: the one-row kernel. Tree rows: each row gathers its own list (decode-kernel
+    // units). Lines of two or more rows (prefill, speculative verify): the shared kernels,
+    // which read each K/V block once for every row and head of a KV head they hold (split
+    // over the list when there are few of them). Every multi-row kernel computes a row with
+    // the same arithmetic, so the choice does not change a bit of the result.
     if (rows == 1 && !tree) {
         Item item{};
         item.row = 0;
         item.nrows = 1;
         item.len = (uint32_t)slots;
         e = row_attention(a, &item, 1, c->ws, c->stream);
-    } else if (tree || short_line) {
-        const uint32_t chunk = CHUNK_MULTI;
+    } else if (tree) {
         Item items[MAX_ITEMS];
-        const uint32_t nitems = short_line ? nline : rows;
-        for (uint32_t i = 0; i < nitems; i++) {
+        for (uint32_t i = 0; i < rows; i++) {
             Item& I = items[i];
             I = Item{};
-            I.row = short_line ? i * per : i;
-            I.nrows = short_line ? std::min(per, rows - I.row) : 1u;
-            const uint64_t upto = tree ? slots : (uint64_t)pos + I.row + 1;
-            const uint64_t longest = upto + I.nrows - 1;
-            I.len = (uint32_t)upto;
-            I.nchunk = (uint32_t)((longest + chunk - 1) / chunk);
-            I.chunk = chunk;
+            I.row = i;
+            I.nrows = 1;
+            I.len = (uint32_t)slots;
+            I.nchunk = (uint32_t)((slots + CHUNK_MULTI - 1) / CHUNK_MULTI);
+            I.chunk = CHUNK_MULTI;
         }
-        e = direct_attention(a, items, nitems, c->ws, c->stream);
+        e = direct_attention(a, items, rows, c->ws, c->stream);
     } else {
         e = shared_attention(a, c->ws, c->stream);
     }
