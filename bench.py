@@ -1,19 +1,22 @@
 """Benchmark of the MI355X attention path (libbchip.so) on BASELINE.json's configurations.
 
 Headline (`value`): configs[1], Llama-3-8B-shaped decode: batch 1, 32 query / 8 KV heads,
-head_dim 128, f16 KV cache at 32768 visible slots, RoPE theta 5e5 fused with the one-row
-K/V append, 32 layers with distinct caches. A step is one token through all 32 layers
-(bchip_rope_append + bchip_attention per layer); value = tokens/s of those steps, with
-inputs resident in HBM. Extras: decode at 1024 and 4096 slots (their 32 layers' caches fit
-the 256 MB MALL: labelled so), causal prefill at 2048 and 8192 tokens (TFLOP/s, configs[2]),
-the Llama-3-70B stage share's verify steps, Qwen2.5-7B ragged batched decode
-(configs[3]).
+head_dim 128, f16 KV cache at 32768 visible slots, RoPE theta 5e5 with the one-row K/V
+append, 32 layers with distinct caches. A step is one token through all 32 layers, each
+layer one bchip_rope_append_attention call (k_rope(q), k_rope(k), k_copy(k), k_copy(v) and
+k_attention of the reference's per-layer sequence, the same bits as bchip_rope_append then
+bchip_attention); value = tokens/s of those steps, inputs resident in HBM. Extras: decode
+at 1024 and 4096 slots (their 32 layers' caches fit the 256 MB MALL: labelled so), causal
+prefill at 2048 and 8192 tokens (TFLOP/s, configs[2]), the Llama-3-70B stage share's
+prefill and verify steps, Qwen2.5-7B ragged batched decode.
 
-roofline: the decode attention call's algorithmic bytes per launch (2 * L * n_kv * hd * 2
-bytes of f16 K and V, each read once) over its mean duration, from HIP events recorded
-around every attention call of the timed region on the library's stream (the call is the
-attn_decode kernel plus the small attn_decode_fold; the events include the gap between
-them). traffic: measured HBM bytes per call from the committed rocprofv3 counter summary.
+roofline: the dominant kernel, the decode attention kernel (attn_decode_row): algorithmic
+bytes per launch (2 * L * n_kv * hd * 2 bytes of f16 K and V, each read once) over its mean
+duration, from HIP events the library records on its stream right before and after that
+kernel (bchip_timer_arm) on every 8th layer's call of the timed region. roofline.call gives
+the same bytes over the whole per-layer call (decode kernel, chunk fold, launch gaps: the
+step time over the layers). traffic: measured HBM bytes per launch from the committed
+rocprofv3 counter summary.
 
 cpu_baseline: bc-infer's CPU attention as the oracle's C restatement (single thread, as
 the reference runs it: crates/bc-infer/src/model.rs:391-403, 448-481), timed on this
@@ -37,6 +40,7 @@ import numpy as np  # noqa: E402
 import bchip  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+EVENT_EVERY = 8  # decode: HIP events bracket the attention call of every 8th layer
 MFMA_F16_PEAK_TFLOPS = 2516.6
 METRIC = "attn decode GB/s & prefill TFLOP/s on 1 MI355X, % of roofline; tokens/s"
 
@@ -123,19 +127,22 @@ class DecodeModel:
         v = k + self.nkv * self.hd * 4
         return q, k, v
 
-    def step(self, step, hip=None, evs=None):
+    def step(self, step, hip=None, evs=None, every=EVENT_EVERY):
+        """One token through every layer: the layer's RoPE + K/V append + attention as one
+        bchip_rope_append_attention call (the same bits as bchip_rope_append followed by
+        bchip_attention). With evs, the calls of every `every`-th layer record a pair of HIP
+        events around their attention kernel (bchip_timer_arm: the library records them on
+        its stream right before and after the kernel); a pair costs a few microseconds of
+        stream time, so it is not put on every call of the step being timed."""
         ctx = self.ctx
         slot = self.ctx_len + step
         for layer in range(self.n_layer):
             q, k, v = self.layer_ptrs(step, layer)
-            ctx.rope_append(q, k, v, self.kc[layer], self.vc[layer], bchip.F16, self.inv, self.pos.ptr + 4 * step, 1,
-                            self.nh, self.nkv, self.hd, self.hd, self.neox, slot)
-            if evs is not None:
-                hip.record(evs[2 * layer], self.stream)
-            ctx.attention(q, self.kc[layer], self.vc[layer], bchip.F16, self.out, None, False, 1, self.nh, self.nkv,
-                          self.hd, slot, 1.0 / math.sqrt(self.hd))
-            if evs is not None:
-                hip.record(evs[2 * layer + 1], self.stream)
+            if evs is not None and layer % every == 0:
+                ctx.timer_arm(evs[2 * (layer // every)], evs[2 * (layer // every) + 1])
+            ctx.rope_append_attention(q, k, v, self.kc[layer], self.vc[layer], bchip.F16, self.inv,
+                                      self.pos.ptr + 4 * step, self.nh, self.nkv, self.hd, self.hd, self.neox, slot,
+                                      1.0 / math.sqrt(self.hd), self.out)
 
     def free(self):
         for b in self.kc + self.vc + [self.qkv, self.out, self.pos, self.inv]:
@@ -148,12 +155,13 @@ def bench_decode(ctx, hip, ctx_len, steps, warmup, n_layer=32, nh=32, nkv=8, hd=
     for s in range(warmup):
         m.step(s)
     ctx.sync()
-    evs = hip.events(2 * n_layer * steps)
+    per_step = n_layer // EVENT_EVERY
+    evs = hip.events(2 * per_step * steps)
     ctx.timer_start()
     for s in range(steps):
-        m.step(warmup + s, hip, evs[2 * n_layer * s: 2 * n_layer * (s + 1)])
+        m.step(warmup + s, hip, evs[2 * per_step * s: 2 * per_step * (s + 1)])
     total_ms = ctx.timer_stop()
-    kernel_ms = [hip.elapsed(evs[2 * i], evs[2 * i + 1]) for i in range(n_layer * steps)]
+    kernel_ms = [hip.elapsed(evs[2 * i], evs[2 * i + 1]) for i in range(per_step * steps)]
     hip.destroy(evs)
     m.free()
     mean_kernel_ms = statistics.fmean(kernel_ms)
@@ -161,10 +169,13 @@ def bench_decode(ctx, hip, ctx_len, steps, warmup, n_layer=32, nh=32, nkv=8, hd=
     mean_len = ctx_len + warmup + (steps - 1) / 2 + 1
     bytes_per_launch = 2 * mean_len * nkv * hd * 2
     gbs = bytes_per_launch / (mean_kernel_ms * 1e-3) / 1e9
+    call_ms = total_ms / steps / n_layer  # one layer's whole call: decode kernel, fold, gaps
     return {
         "ctx": ctx_len, "layers": n_layer, "steps": steps, "ms_per_step": total_ms / steps,
-        "tokens_per_s": steps / (total_ms * 1e-3), "attn_launch_us": mean_kernel_ms * 1e3,
+        "tokens_per_s": steps / (total_ms * 1e-3), "attn_kernel_us": mean_kernel_ms * 1e3,
         "attn_bytes_per_launch": bytes_per_launch, "attn_GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+        "call_us": call_ms * 1e3, "call_GBps": bytes_per_launch / (call_ms * 1e-3) / 1e9,
+        "call_hbm_frac": bytes_per_launch / (call_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
     }
 
 
@@ -187,30 +198,36 @@ def bench_multirow(ctx, hip, rows, pos, nh, nkv, hd, reps, n_layer=1, verify=Fal
     for layer in range(n_layer):
         ctx.attention(q, kcs[layer], vcs[layer], bchip.F16, out, None, False, rows, nh, nkv, hd, pos, scale)
     ctx.sync()
-    evs = hip.events(2 * reps * n_layer)
+    evs = hip.events(4 * reps * n_layer)  # per call: outer pair (the call), inner pair (its kernel)
     i = 0
     ctx.timer_start()
     for r in range(reps):
         for layer in range(n_layer):
             hip.record(evs[i], stream)
+            ctx.timer_arm(evs[i + 2], evs[i + 3])
             ctx.attention(q, kcs[layer], vcs[layer], bchip.F16, out, None, False, rows, nh, nkv, hd, pos, scale)
             hip.record(evs[i + 1], stream)
-            i += 2
+            i += 4
     total_ms = ctx.timer_stop()
-    per = [hip.elapsed(evs[2 * j], evs[2 * j + 1]) for j in range(reps * n_layer)]
+    per_call = [hip.elapsed(evs[4 * j], evs[4 * j + 1]) for j in range(reps * n_layer)]
+    per_kernel = [hip.elapsed(evs[4 * j + 2], evs[4 * j + 3]) for j in range(reps * n_layer)]
     hip.destroy(evs)
     for b in kcs + vcs + [q, out]:
         b.free()
     pairs = rows * pos + rows * (rows + 1) / 2  # unmasked (query, key) pairs
     flops = 4.0 * hd * nh * pairs
     kv_bytes = 2.0 * slots * kvd * 2
-    us = statistics.fmean(per) * 1e3
-    res = {"rows": rows, "pos": pos, "heads": [nh, nkv, hd], "layers": n_layer, "launch_us": us,
+    us = statistics.fmean(per_kernel) * 1e3
+    call_us = statistics.fmean(per_call) * 1e3
+    res = {"rows": rows, "pos": pos, "heads": [nh, nkv, hd], "layers": n_layer, "kernel_us": us, "call_us": call_us,
            "ms_per_pass": total_ms / reps, "TFLOPs": flops / (us * 1e-6) / 1e12,
-           "mfma_frac": flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS}
+           "mfma_frac": flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS,
+           "call_TFLOPs": flops / (call_us * 1e-6) / 1e12,
+           "call_mfma_frac": flops / (call_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS}
     if verify:
         res["GBps"] = kv_bytes / (us * 1e-6) / 1e9
         res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
+        res["call_GBps"] = kv_bytes / (call_us * 1e-6) / 1e9
     return res
 
 
@@ -237,25 +254,30 @@ def bench_ragged(ctx, hip, reps):
     for layer in range(n_layer):
         ctx.attention_ragged(q, kcs[layer], vcs[layer], bchip.F16, out, lens, offs, nh, nkv, hd, 0.0884)
     ctx.sync()
-    evs = hip.events(2 * reps * n_layer)
+    evs = hip.events(4 * reps * n_layer)  # per call: outer pair (the call), inner pair (its kernel)
     i = 0
     ctx.timer_start()
     for r in range(reps):
         for layer in range(n_layer):
             hip.record(evs[i], stream)
+            ctx.timer_arm(evs[i + 2], evs[i + 3])
             ctx.attention_ragged(q, kcs[layer], vcs[layer], bchip.F16, out, lens, offs, nh, nkv, hd, 0.0884)
             hip.record(evs[i + 1], stream)
-            i += 2
+            i += 4
     total_ms = ctx.timer_stop()
-    per = [hip.elapsed(evs[2 * j], evs[2 * j + 1]) for j in range(reps * n_layer)]
+    per_call = [hip.elapsed(evs[4 * j], evs[4 * j + 1]) for j in range(reps * n_layer)]
+    per_kernel = [hip.elapsed(evs[4 * j + 2], evs[4 * j + 3]) for j in range(reps * n_layer)]
     hip.destroy(evs)
     for b in kcs + vcs + [q, out]:
         b.free()
-    us = statistics.fmean(per) * 1e3
+    us = statistics.fmean(per_kernel) * 1e3
+    call_us = statistics.fmean(per_call) * 1e3
     bytes_ = 2.0 * total * kvd * 2
-    return {"seqs": 16, "total_slots": total, "layers": n_layer, "launch_us": us, "ms_per_step": total_ms / reps,
-            "tokens_per_s": 16 * reps / (total_ms * 1e-3), "GBps": bytes_ / (us * 1e-6) / 1e9,
-            "hbm_frac": bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    return {"seqs": 16, "total_slots": total, "layers": n_layer, "kernel_us": us, "call_us": call_us,
+            "ms_per_step": total_ms / reps, "tokens_per_s": 16 * reps / (total_ms * 1e-3),
+            "GBps": bytes_ / (us * 1e-6) / 1e9, "hbm_frac": bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "call_GBps": bytes_ / (call_us * 1e-6) / 1e9,
+            "call_hbm_frac": bytes_ / (call_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
 def bench_copy_calibration(ctx, hip, mib=256, reps=4):
@@ -403,8 +425,10 @@ def main():
                      "frac": head["hbm_frac"], "traffic": profiled_traffic(args.ctx),
                      "traffic_source": "profiles/attn_decode_llama8b_32k.txt (rocprofv3 FETCH_SIZE x 2.0 + "
                                        "WRITE_SIZE x 1.0, factors from a 256 MiB copy)",
-                     "kernel": "bchip attention (rows=1 decode)",
-                     "bytes_per_launch": head["attn_bytes_per_launch"], "launch_us": head["attn_launch_us"]},
+                     "kernel": "attn_decode_row<128, f16, fused> (bchip_rope_append_attention's attention kernel)",
+                     "bytes_per_launch": head["attn_bytes_per_launch"], "launch_us": head["attn_kernel_us"],
+                     "call": {"what": "the whole per-layer call: decode kernel, chunk fold, launch gaps",
+                              "us": head["call_us"], "GBps": head["call_GBps"], "frac": head["call_hbm_frac"]}},
         "cpu_baseline": cpu,
         "extra": extra,
     }

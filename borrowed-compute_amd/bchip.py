@@ -65,10 +65,12 @@ def lib() -> ctypes.CDLL:
         "bchip_keep": ([P, P, u32, u32, u32, u64, P, u32], i32),
         "bchip_rope_append": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, u64], i32),
         "bchip_attention": ([P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32], i32),
+        "bchip_rope_append_attention": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32, P], i32),
         "bchip_attention_ragged": ([P, P, P, P, u32, P, P, P, u32, u32, u32, u32, f32], i32),
         "bchip_fill_normal": ([P, P, u32, u64, u64], i32),
         "bchip_timer_start": ([P], i32),
         "bchip_timer_stop": ([P, P], i32),
+        "bchip_timer_arm": ([P, P, P], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -196,6 +198,12 @@ class Ctx:
         check(lib().bchip_attention(self.h, _ptr(q), _ptr(kc), _ptr(vc), kv_type, _ptr(out), _ptr(masks),
                                     int(tree), rows, nh, nkv, hd, pos, scale))
 
+    def rope_append_attention(self, q, k, v, kc, vc, kv_type, inv_freq, positions, nh, nkv, hd, rope_dim, neox,
+                              pos, scale, out) -> None:
+        check(lib().bchip_rope_append_attention(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc), kv_type,
+                                                _ptr(inv_freq), _ptr(positions), nh, nkv, hd, rope_dim, int(neox),
+                                                pos, scale, _ptr(out)))
+
     def attention_ragged(self, q, kc, vc, kv_type, out, seq_lens, kv_offsets, nh, nkv, hd, scale) -> None:
         lens = np.ascontiguousarray(seq_lens, np.uint32)
         offs = np.ascontiguousarray(kv_offsets, np.uint64)
@@ -208,6 +216,10 @@ class Ctx:
 
     def timer_start(self) -> None:
         check(lib().bchip_timer_start(self.h))
+
+    def timer_arm(self, before, after) -> None:
+        """The next attention call records these hipEvent_t around its main kernel."""
+        check(lib().bchip_timer_arm(self.h, before, after))
 
     def timer_stop(self) -> float:
         ms = ctypes.c_float()

@@ -256,6 +256,10 @@ struct Raw<f16> {
     __device__ __forceinline__ void load(const f16* p) { v = *(const half8*)p; }
     // A load marked as streaming (read once: kept out of the caches' reuse).
     __device__ __forceinline__ void load_stream(const f16* p) { v = __builtin_nontemporal_load((const half8*)p); }
+    // Eight f32 values as the cache would hold them.
+    __device__ __forceinline__ void set(float4 x, float4 y) {
+        v = half8{(f16)x.x, (f16)x.y, (f16)x.z, (f16)x.w, (f16)y.x, (f16)y.y, (f16)y.z, (f16)y.w};
+    }
     __device__ __forceinline__ half8 get() const { return v; }
 };
 template <>
@@ -269,6 +273,10 @@ struct Raw<float> {
         const f32x4 x = __builtin_nontemporal_load((const f32x4*)p), y = __builtin_nontemporal_load((const f32x4*)(p + 4));
         a = float4{x[0], x[1], x[2], x[3]};
         b = float4{y[0], y[1], y[2], y[3]};
+    }
+    __device__ __forceinline__ void set(float4 x, float4 y) {
+        a = x;
+        b = y;
     }
     __device__ __forceinline__ half8 get() const {
         return half8{(f16)a.x, (f16)a.y, (f16)a.z, (f16)a.w, (f16)b.x, (f16)b.y, (f16)b.z, (f16)b.w};
@@ -538,7 +546,7 @@ constexpr int RB = 32;                     // list entries per block of the one-
 constexpr uint32_t ROW_MAX_CHUNKS = 256;   // chunks per (item, KV head): attn_row_fold's reach
 constexpr uint32_t ROW_FOLD_BATCH = 16;    // chunk states a thread loads before folding them
 
-template <int HD, typename KVT>
+template <int HD, typename KVT, bool FUSE>
 __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) {
     constexpr int NKC = HD / 32;        // hd chunks of a score MFMA
     constexpr int NDT = HD / 16;        // output tiles of 16 dims
@@ -562,21 +570,6 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
     const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
 
-    // Q^T operands (B of the score MFMAs), straight into registers.
-    half8 qb[NKC];
-    {
-        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * G + (valid ? n : 0)) * hd;
-        float4 qa[NKC], qc[NKC];
-#pragma unroll
-        for (int c2 = 0; c2 < NKC; c2++) {
-            const uint32_t hd0 = 32 * c2 + 8 * g;
-            const float* src = (valid && hd0 < hd) ? qrow + hd0 : (const float*)p.zero;
-            qa[c2] = *(const float4*)src;
-            qc[c2] = *(const float4*)(src + 4);
-        }
-#pragma unroll
-        for (int c2 = 0; c2 < NKC; c2++) qb[c2] = q_scaled(qa[c2], qc[c2], p.sc);
-    }
     // Block key0 into registers; entries at or past kb1 read the zero page (no HBM traffic,
     // no branch between the loads).
     auto load_block = [&](uint32_t key0, Raw<KVT> (&kr)[2][NKC], Raw<KVT> (&vr)[NVL]) {
@@ -597,20 +590,124 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
             vr[i].load_stream((key < kb1 && d < hd) ? vc + (size_t)key * kvd + d : zp);
         }
     };
+    // Q^T operands (B of the score MFMAs), straight into registers; fused with RoPE, the
+    // wave first rotates its G heads into its LDS tile, one pair per lane, and takes the
+    // operands from there.
+    half8 qb[NKC];
+    f16* vw = vl[w];
+    const uint32_t newslot = I.len - 1;
+    const bool has_new = FUSE && newslot >= kb0 && newslot < kb1;  // this chunk holds the new row
+    Raw<KVT> kn[NKC], vn;  // the new row's K operands and V elements, as the cache holds them
+    // The first block's loads go out before anything else (double-buffered path).
+    constexpr bool DB = sizeof(KVT) == 2 && HD <= 128;
+    Raw<KVT> kA[2][NKC], vA[NVL], kB[2][NKC], vB[NVL];
+    if constexpr (DB) load_block(kb0, kA, vA);
+    if constexpr (FUSE) {
+        float* qs = (float*)vw;  // [G][HD] rotated q, then [HD] rotated k of the new row
+        // Lane pairs pp = lane + 64j: the angle depends on the pair alone, so its sine and
+        // cosine serve all G heads and the new K row.
+        constexpr int NPJ = (HD / 2 + 63) / 64;
+        const float posf = (float)p.positions[0];
+        const uint32_t half = hd / 2;
+        float sn[NPJ], cs[NPJ];
+        uint32_t pa[NPJ], pb[NPJ];
+        bool prot[NPJ];
+#pragma unroll
+        for (int j = 0; j < NPJ; j++) {
+            const uint32_t pp = lane + 64 * j;
+            prot[j] = pp < half && rope_pair(pp, p.rope_dim, p.neox, pa[j], pb[j]);
+            if (pp >= half) pa[j] = pb[j] = 0;
+            sn[j] = 0.0f;
+            cs[j] = 1.0f;
+            if (prot[j]) sincosf(posf * p.inv_freq[pp], &sn[j], &cs[j]);
+        }
+        for (uint32_t h = 0; h < G; h++) {
+            const float* qr = p.q + ((size_t)I.row * p.nh + kvh * G + h) * hd;
+#pragma unroll
+            for (int j = 0; j < NPJ; j++) {
+                if (lane + 64 * j >= half) continue;
+                float y0 = qr[pa[j]], y1 = qr[pb[j]];
+                if (prot[j]) rotate_sc(qr[pa[j]], qr[pb[j]], sn[j], cs[j], y0, y1);
+                qs[h * HD + pa[j]] = y0;
+                qs[h * HD + pb[j]] = y1;
+            }
+        }
+        if (has_new) {
+            const float* kr = p.knew + (size_t)kvh * hd;
+            KVT* kdst = (KVT*)p.kc + (I.kvoff + newslot) * kvd + (size_t)kvh * hd;
+#pragma unroll
+            for (int j = 0; j < NPJ; j++) {
+                if (lane + 64 * j >= half) continue;
+                float y0 = kr[pa[j]], y1 = kr[pb[j]];
+                if (prot[j]) rotate_sc(kr[pa[j]], kr[pb[j]], sn[j], cs[j], y0, y1);
+                qs[G * HD + pa[j]] = y0;
+                qs[G * HD + pb[j]] = y1;
+                kdst[pa[j]] = to_kv<KVT>(y0);
+                kdst[pb[j]] = to_kv<KVT>(y1);
+            }
+            const float* vr = p.vnew + (size_t)kvh * hd;
+            KVT* vdst = (KVT*)p.vc + (I.kvoff + newslot) * kvd + (size_t)kvh * hd;
+            for (uint32_t e = lane; e < hd; e += 64) vdst[e] = to_kv<KVT>(vr[e]);
+            const float4 z = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c2 = 0; c2 < NKC; c2++) {
+                const uint32_t hd0 = 32 * c2 + 8 * g;
+                kn[c2].set(hd0 < hd ? *(const float4*)&qs[G * HD + hd0] : z, hd0 < hd ? *(const float4*)&qs[G * HD + hd0 + 4] : z);
+            }
+            const uint32_t d = 8 * (lane % VLR);
+            vn.set(d < hd ? *(const float4*)(vr + d) : z, d < hd ? *(const float4*)(vr + d + 4) : z);
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < NKC; c2++) {
+            const uint32_t hd0 = 32 * c2 + 8 * g;
+            const bool ok = valid && hd0 < hd;
+            const float4 z = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            qb[c2] = q_scaled(ok ? *(const float4*)&qs[n * HD + hd0] : z, ok ? *(const float4*)&qs[n * HD + hd0 + 4] : z, p.sc);
+        }
+        // q stays rotated, as k_rope leaves it. Other units of this KV head may still be
+        // reading it, so with several chunks the first one stages the rotated heads and
+        // attn_row_fold, which runs after every unit, copies them into q; a lone unit writes q.
+        if (c == 0) {
+            float* dst = I.nchunk == 1 ? p.qw + (size_t)I.row * p.nh * hd : p.qrot;
+            for (uint32_t e = lane; e < G * hd; e += 64) {
+                const uint32_t h = e / hd, d = e % hd;
+                dst[(size_t)(kvh * G + h) * hd + d] = qs[h * HD + d];
+            }
+        }
+    } else {
+        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * G + (valid ? n : 0)) * hd;
+        float4 qa[NKC], qc[NKC];
+#pragma unroll
+        for (int c2 = 0; c2 < NKC; c2++) {
+            const uint32_t hd0 = 32 * c2 + 8 * g;
+            const float* src = (valid && hd0 < hd) ? qrow + hd0 : (const float*)p.zero;
+            qa[c2] = *(const float4*)src;
+            qc[c2] = *(const float4*)(src + 4);
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < NKC; c2++) qb[c2] = q_scaled(qa[c2], qc[c2], p.sc);
+    }
     f32x4 o[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
-    f16* vw = vl[w];
-    auto compute_block = [&](uint32_t key0, const Raw<KVT> (&kr)[2][NKC], const Raw<KVT> (&vr)[NVL]) {
+    // SUB: the block holding the new row (fused steps), whose lanes on that row take kn, vn
+    // in place of what they loaded.
+    auto compute_block = [&](uint32_t key0, const Raw<KVT> (&kr)[2][NKC], const Raw<KVT> (&vr)[NVL], auto SUB) {
+        constexpr bool sub = decltype(SUB)::value;
 #pragma unroll
-        for (int i = 0; i < NVL; i++) v_store<VS>(vw, i * VRI + lane / VLR, 8 * (lane % VLR), vr[i].get());
+        for (int i = 0; i < NVL; i++) {
+            half8 v = vr[i].get();
+            if constexpr (sub) v = (key0 + i * VRI + lane / VLR == newslot) ? vn.get() : v;
+            v_store<VS>(vw, i * VRI + lane / VLR, 8 * (lane % VLR), v);
+        }
         f32x4 st[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const bool mine = sub && key0 + 16 * t + n == newslot;
 #pragma unroll
-            for (int c2 = 0; c2 < NKC; c2++) st[t] = mfma16(kr[t][c2].get(), qb[c2], st[t]);
+            for (int c2 = 0; c2 < NKC; c2++) st[t] = mfma16(mine ? kn[c2].get() : kr[t][c2].get(), qb[c2], st[t]);
         }
         float x[2][4], mx = -INFINITY;
 #pragma unroll
@@ -644,24 +741,27 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     // Two register sets in turn where they fit (f16, hd <= 128): the next block loads while
     // this one computes. Wider rows load and compute one block at a time; the other resident
     // waves of the CU still overlap them.
-    if constexpr (sizeof(KVT) == 2 && HD <= 128) {
-        Raw<KVT> kA[2][NKC], vA[NVL], kB[2][NKC], vB[NVL];
-        load_block(kb0, kA, vA);
+    auto compute = [&](uint32_t key0, const Raw<KVT> (&kr)[2][NKC], const Raw<KVT> (&vr)[NVL]) {
+        if (FUSE && has_new && newslot - key0 < (uint32_t)RB)
+            compute_block(key0, kr, vr, std::integral_constant<bool, FUSE>{});
+        else
+            compute_block(key0, kr, vr, std::false_type{});
+    };
+    if constexpr (DB) {
         for (uint32_t key0 = kb0;;) {
             load_block(key0 + RB, kB, vB);
-            compute_block(key0, kA, vA);
+            compute(key0, kA, vA);
             key0 += RB;
             if (key0 >= kb1) break;
             load_block(key0 + RB, kA, vA);
-            compute_block(key0, kB, vB);
+            compute(key0, kB, vB);
             key0 += RB;
             if (key0 >= kb1) break;
         }
     } else {
-        Raw<KVT> kA[2][NKC], vA[NVL];
         for (uint32_t key0 = kb0; key0 < kb1; key0 += RB) {
             load_block(key0, kA, vA);
-            compute_block(key0, kA, vA);
+            compute(key0, kA, vA);
         }
     }
     if (!valid) return;
@@ -702,6 +802,12 @@ __global__ __launch_bounds__(256) void attn_row_fold(const DirectParams p) {
     if (nch <= 1) return;  // written by the decode kernel
     const uint32_t kvh = (b % per_item) / p.G, s = (b % per_item) % p.G;
     const uint32_t tid = threadIdx.x, r = tid / D4, d = 4 * (tid % D4);
+    if (p.fuse) {
+        // A fused step: every unit has read q; leave head kvh * G + s rotated.
+        const size_t h = (size_t)kvh * p.G + s;
+        for (uint32_t e = tid; e < p.hd; e += 256) p.qw[((size_t)I.row * p.nh + h) * p.hd + e] = p.qrot[h * p.hd + e];
+    }
+
     const uint32_t c0 = r * nch / R, c1 = (r + 1) * nch / R;
     const size_t cu0 = (size_t)I.unit0 + (size_t)kvh * nch;
     float M = -INFINITY, L = 0.0f;
@@ -1342,21 +1448,30 @@ template <int HD>
 static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s);
 
 template <int HD, typename KVT>
-static hipError_t launch_decode_t(DirectParams& dp, CombineParams& cp, hipStream_t s) {
+static hipError_t launch_decode_t(DirectParams& dp, CombineParams& cp, const AttnCall& a, hipStream_t s) {
     const dim3 block(256);
+    hipError_t e = mark(a.ev_before, s);
+    if (e != hipSuccess) return e;
     if (dp.tree)
         hipLaunchKernelGGL((attn_decode<HD, KVT, true>), dim3(dp.nunits), block, 0, s, dp);
     else
         hipLaunchKernelGGL((attn_decode<HD, KVT, false>), dim3(dp.nunits), block, 0, s, dp);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
+    if (e == hipSuccess) e = mark(a.ev_after, s);
     if (e != hipSuccess) return e;
     return launch_combine_t<HD>(cp, dp.nitems * dp.nkv, s);
 }
 
 template <int HD, typename KVT>
-static hipError_t launch_row_t(const DirectParams& dp, bool fold, hipStream_t s) {
-    hipLaunchKernelGGL((attn_decode_row<HD, KVT>), dim3(ceil_div(dp.nunits, 4)), dim3(256), 0, s, dp);
-    hipError_t e = hipGetLastError();
+static hipError_t launch_row_t(const DirectParams& dp, bool fold, const AttnCall& a, hipStream_t s) {
+    hipError_t e = mark(a.ev_before, s);
+    if (e != hipSuccess) return e;
+    if (dp.fuse)
+        hipLaunchKernelGGL((attn_decode_row<HD, KVT, true>), dim3(ceil_div(dp.nunits, 4)), dim3(256), 0, s, dp);
+    else
+        hipLaunchKernelGGL((attn_decode_row<HD, KVT, false>), dim3(ceil_div(dp.nunits, 4)), dim3(256), 0, s, dp);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = mark(a.ev_after, s);
     if (e != hipSuccess || !fold) return e;
     hipLaunchKernelGGL((attn_row_fold<HD>), dim3(dp.nitems * dp.nkv * dp.G), dim3(256), 0, s, dp);
     return hipGetLastError();
@@ -1398,10 +1513,42 @@ uint32_t row_chunk(uint64_t len, uint32_t nkv) {
     return (uint32_t)std::max<uint64_t>(chunk, 2 * RB);
 }
 
+bool row_fusable(uint32_t hd, uint32_t rope_dim, uint32_t neox) {
+    // Every rotated pair's two dims sit in one lane's operand groups (dims 32c + 8g + j).
+    return hd % 32 == 0 && hd <= MAX_HD && rope_dim % 2 == 0 && rope_dim <= hd && (!neox || (rope_dim / 2) % 32 == 0);
+}
+
+static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nitems, const RopeArgs* rope,
+                             Workspace& ws, hipStream_t s);
+
 hipError_t row_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s) {
+    return row_launch(a, items, nitems, nullptr, ws, s);
+}
+
+hipError_t row_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s) {
+    if (!row_fusable(a.hd, r.rope_dim, r.neox)) return hipErrorInvalidValue;
+    Item item{};
+    item.row = 0;
+    item.nrows = 1;
+    item.len = a.pos + 1;
+    return row_launch(a, &item, 1, &r, ws, s);
+}
+
+static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nitems, const RopeArgs* rope,
+                             Workspace& ws, hipStream_t s) {
     if (nitems == 0 || nitems > MAX_ITEMS) return hipErrorInvalidValue;
     DirectParams dp = direct_params(a, ws, nitems);
     dp.tree = 0;
+    if (rope) {
+        dp.fuse = 1;
+        dp.qw = rope->q;
+        dp.knew = rope->k;
+        dp.vnew = rope->v;
+        dp.inv_freq = rope->inv_freq;
+        dp.positions = rope->positions;
+        dp.rope_dim = rope->rope_dim;
+        dp.neox = rope->neox;
+    }
     uint64_t units = 0;
     bool fold = false;
     for (uint32_t i = 0; i < nitems; i++) {
@@ -1419,13 +1566,15 @@ hipError_t row_attention(const AttnCall& a, const Item* items, uint32_t nitems, 
     dp.nunits = (uint32_t)units;
     const int hdp = pad_hd(a.hd);
     hipError_t e = ws.reserve((size_t)units * 16, (size_t)hdp);
+    if (e == hipSuccess && rope) e = ws.reserve_qrot((size_t)a.nh * a.hd);
     if (e != hipSuccess) return e;
     dp.part_o = ws.o;
     dp.part_ml = ws.ml;
+    dp.qrot = ws.qrot;
     if (a.kv_type == 1) {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, f16>(dp, fold, s)));
+        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, f16>(dp, fold, a, s)));
     } else {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, float>(dp, fold, s)));
+        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, float>(dp, fold, a, s)));
     }
     return e;
 }
@@ -1464,9 +1613,9 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
     cp.nitems = nitems;
     for (uint32_t i = 0; i < nitems; i++) cp.items[i] = dp.items[i];
     if (a.kv_type == 1) {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, f16>(dp, cp, s)));
+        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, f16>(dp, cp, a, s)));
     } else {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, float>(dp, cp, s)));
+        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, float>(dp, cp, a, s)));
     }
     return e;
 }
@@ -1517,26 +1666,36 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
             hipLaunchKernelGGL(vt_pack, dim3(nb, a.nkv), dim3(256), 0, s, (const f16*)a.vc,
                                (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, sp.vt_npad);
             e = hipGetLastError();
+            if (e == hipSuccess) e = mark(a.ev_before, s);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((attn_prefill<8, true, 4>), dim3(blocks), dim3(512), 0, s, sp);
-        } else if (wide) {
-            hipLaunchKernelGGL((attn_prefill<8, false, 4>), dim3(blocks), dim3(512), 0, s, sp);
         } else {
-            hipLaunchKernelGGL((attn_prefill<4, false, 4>), dim3(blocks), dim3(256), 0, s, sp);
+            e = mark(a.ev_before, s);
+            if (e != hipSuccess) return e;
+            if (wide)
+                hipLaunchKernelGGL((attn_prefill<8, false, 4>), dim3(blocks), dim3(512), 0, s, sp);
+            else
+                hipLaunchKernelGGL((attn_prefill<4, false, 4>), dim3(blocks), dim3(256), 0, s, sp);
         }
         e = hipGetLastError();
-    } else if (a.kv_type == 1) {
-        if (wide) {
-            BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, s)));
-        } else {
-            BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, 1>(sp, blocks, s)));
-        }
+        if (e == hipSuccess) e = mark(a.ev_after, s);
     } else {
-        if (wide) {
-            BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, s)));
+        e = mark(a.ev_before, s);
+        if (e != hipSuccess) return e;
+        if (a.kv_type == 1) {
+            if (wide) {
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, s)));
+            } else {
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, 1>(sp, blocks, s)));
+            }
         } else {
-            BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, 1>(sp, blocks, s)));
+            if (wide) {
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, s)));
+            } else {
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, 1>(sp, blocks, s)));
+            }
         }
+        if (e == hipSuccess) e = mark(a.ev_after, s);
     }
     if (e != hipSuccess || !sp.split) return e;
     CombineParams cp{};

@@ -31,6 +31,13 @@ struct bchip_ctx {
     Workspace ws;
     std::map<uintptr_t, size_t> allocs;  // base -> bytes, of bchip_alloc memory
     std::string name;
+    hipEvent_t arm_before = nullptr, arm_after = nullptr;  // bchip_timer_arm, for the next call
+    // The armed events, handed to one attention call and cleared.
+    void take_marks(bchip::AttnCall& a) {
+        a.ev_before = arm_before;
+        a.ev_after = arm_after;
+        arm_before = arm_after = nullptr;
+    }
 };
 
 namespace {
@@ -141,6 +148,17 @@ hipError_t Workspace::reserve_vt(size_t bytes) {
     return hipSuccess;
 }
 
+hipError_t Workspace::reserve_qrot(size_t floats) {
+    if (floats <= qrot_floats && qrot) return hipSuccess;
+    if (qrot) (void)hipFree(qrot);
+    qrot = nullptr;
+    qrot_floats = 0;
+    hipError_t e = hipMalloc((void**)&qrot, floats * sizeof(float));
+    if (e != hipSuccess) return e;
+    qrot_floats = floats;
+    return hipSuccess;
+}
+
 hipError_t Workspace::init() {
     hipError_t e = hipMalloc(&zero, ZERO_BYTES);
     if (e != hipSuccess) return e;
@@ -151,8 +169,11 @@ void Workspace::release() {
     if (o) (void)hipFree(o);
     if (ml) (void)hipFree(ml);
     if (vt) (void)hipFree(vt);
+    if (qrot) (void)hipFree(qrot);
     o = ml = nullptr;
     vt = nullptr;
+    qrot = nullptr;
+    qrot_floats = 0;
     vt_bytes = 0;
     slots = hdp = 0;
 }
@@ -392,6 +413,7 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     const uint64_t row_bytes = kvd * esize(kv_type);
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / row_bytes;
     AttnCall a{q, kc, vc, kv_type, out, masks, tree ? 1u : 0u, rows, nh, nkv, hd, pos, scale, limit};
+    c->take_marks(a);
     hipError_t e;
     // One row: the one-row kernel. Tree rows: each row gathers its own list (decode-kernel
     // units). Lines of two or more rows (prefill, speculative verify): the shared kernels,
@@ -423,6 +445,39 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     return BCHIP_OK;
 }
 
+int bchip_rope_append_attention(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc,
+                                uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,
+                                uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos,
+                                float scale, float* out) {
+    CHECK(enter(c));
+    if (!q || !k || !v || !kc || !vc || !inv_freq || !positions || !out) return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    CHECK(check_heads(nh, nkv, hd));
+    if (rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
+    if (!row_fusable(hd, rope_dim, neox)) {
+        CHECK(bchip_rope_append(c, q, k, v, kc, vc, kv_type, inv_freq, positions, 1, nh, nkv, hd, rope_dim, neox, pos));
+        return bchip_attention(c, q, kc, vc, kv_type, out, nullptr, 0, 1, nh, nkv, hd, pos, scale);
+    }
+    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc) || !aligned16(k) || !aligned16(v))
+        return fail(BCHIP_E_ARG, "q, k, v, out and the caches must be 16-byte aligned");
+    if ((uint64_t)pos + 1 > 0xffffffffull) return fail(BCHIP_E_ARG, "position past 2^32");
+    const uint64_t kvd = (uint64_t)nkv * hd, slots = (uint64_t)pos + 1;
+    CHECK(check_span(c, q, (uint64_t)nh * hd * 4, "q"));
+    CHECK(check_span(c, out, (uint64_t)nh * hd * 4, "out"));
+    CHECK(check_span(c, k, kvd * 4, "k"));
+    CHECK(check_span(c, v, kvd * 4, "v"));
+    CHECK(check_span(c, kc, slots * kvd * esize(kv_type), "kc"));
+    CHECK(check_span(c, vc, slots * kvd * esize(kv_type), "vc"));
+    CHECK(check_span(c, positions, 4, "positions"));
+    CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
+    const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
+    AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, pos, scale, limit};
+    c->take_marks(a);
+    RopeArgs r{q, k, v, inv_freq, positions, rope_dim, neox};
+    HIP_TRY(row_attention_fused(a, r, c->ws, c->stream), "rope_append_attention");
+    return BCHIP_OK;
+}
+
 int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const void* vc, uint32_t kv_type,
                            float* out, const uint32_t* seq_lens, const uint64_t* kv_offsets, uint32_t nseq,
                            uint32_t nh, uint32_t nkv, uint32_t hd, float scale) {
@@ -445,6 +500,7 @@ int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const v
     }
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
     AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, 0u, scale, limit};
+    c->take_marks(a);
     for (uint32_t s0 = 0; s0 < nseq; s0 += MAX_ITEMS) {
         const uint32_t ns = std::min<uint32_t>(MAX_ITEMS, nseq - s0);
         Item items[MAX_ITEMS];
@@ -474,6 +530,14 @@ int bchip_fill_normal(bchip_ctx* c, void* dst, uint32_t type, uint64_t n, uint64
 int bchip_timer_start(bchip_ctx* c) {
     CHECK(enter(c));
     HIP_TRY(hipEventRecord(c->t0, c->stream), "hipEventRecord");
+    return BCHIP_OK;
+}
+
+int bchip_timer_arm(bchip_ctx* c, void* before, void* after) {
+    CHECK(enter(c));
+    if (!before || !after) return fail(BCHIP_E_ARG, "null event");
+    c->arm_before = (hipEvent_t)before;
+    c->arm_after = (hipEvent_t)after;
     return BCHIP_OK;
 }
 

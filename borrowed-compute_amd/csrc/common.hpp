@@ -34,6 +34,41 @@ __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// The rotation of one RoPE pair by theta: y0 = x0 cos - x1 sin, y1 = x0 sin + x1 cos, each
+// product rounded on its own (model.rs:395-400), sincosf the device library's full-range
+// one. Every kernel that rotates uses this, so a row rotated anywhere has the same bits.
+__device__ __forceinline__ void rotate_sc(float x0, float x1, float s, float c, float& y0, float& y1) {
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+__device__ __forceinline__ void rotate(float x0, float x1, float theta, float& y0, float& y1) {
+    float s, c;
+    sincosf(theta, &s, &c);
+    rotate_sc(x0, x1, s, c, y0, y1);
+}
+
+// Dims (a, b) of RoPE pair pp of a head of hd dims: a rotated pair when pp < rope_dim/2
+// (neox: (pp, pp + rope_dim/2), else (2pp, 2pp+1)), else two dims past rope_dim, unrotated.
+__device__ __forceinline__ bool rope_pair(uint32_t pp, uint32_t rope_dim, uint32_t neox, uint32_t& a, uint32_t& b) {
+    const uint32_t hh = rope_dim / 2;
+    const bool rot = pp < hh;
+    a = rot ? (neox ? pp : 2 * pp) : rope_dim + 2 * (pp - hh);
+    b = rot ? (neox ? pp + hh : 2 * pp + 1) : a + 1;
+    return rot;
+}
+
+// A cache element from f32: f16 rounds to nearest even.
+template <typename KVT>
+__device__ __forceinline__ KVT to_kv(float v);
+template <>
+__device__ __forceinline__ f16 to_kv<f16>(float v) {
+    return (f16)v;
+}
+template <>
+__device__ __forceinline__ float to_kv<float>(float v) {
+    return v;
+}
+
 // A row of work for the decode kernel: the G query heads of one row against each KV head.
 // Its list is cut into nchunk chunks of `chunk` entries, one unit of work each per KV head.
 struct Item {
@@ -63,6 +98,18 @@ struct DirectParams {
     uint32_t tree;
     uint64_t slot_limit; // slots the caches hold (tree slots past it read as absent)
     float sc;       // scale * log2(e)
+    // One-row steps fused with RoPE and the K/V append of the new row (fuse != 0): q is
+    // unrotated on entry and rotated in registers (qw receives the rotated q, as k_rope
+    // leaves it); the new K row (knew, f32, rotated here) and V row (vnew) are written to
+    // the caches at the item's last slot and used in place of reading that slot.
+    uint32_t fuse;
+    float* qw;
+    const float* knew;
+    const float* vnew;
+    const float* inv_freq;
+    const uint32_t* positions;  // positions[0]: the rotation's position
+    uint32_t rope_dim, neox;
+    float* qrot;                // [nh][hd]: the rotated q, staged for attn_row_fold to copy into qw
     uint32_t nitems;
     Item items[MAX_ITEMS];
 };

@@ -15,9 +15,11 @@ struct Workspace {
     float* ml = nullptr;   // [units*slots][2]
     void* zero = nullptr;  // ZERO_BYTES of zeros
     void* vt = nullptr;    // V^T tiles of a prefill call
-    size_t slots = 0, hdp = 0, vt_bytes = 0;
+    float* qrot = nullptr;  // rotated q of a fused step, until attn_row_fold copies it
+    size_t slots = 0, hdp = 0, vt_bytes = 0, qrot_floats = 0;
     hipError_t init();     // allocates the zero page
     hipError_t reserve(size_t need_slots, size_t hd_pad);
+    hipError_t reserve_qrot(size_t floats);
     hipError_t reserve_vt(size_t bytes);
     void release();
 };
@@ -34,10 +36,29 @@ struct AttnCall {
     uint32_t tree, rows, nh, nkv, hd, pos;
     float scale;
     uint64_t slot_limit;  // slots both caches hold (all slots a call may read when unknown)
+    // Timing: when set, recorded on the stream right before and right after the call's main
+    // attention kernel (not the V^T pack before it nor the fold or combine after it).
+    hipEvent_t ev_before = nullptr, ev_after = nullptr;
 };
+
+// Records ev on s when it is set (the calls' timing marks).
+inline hipError_t mark(hipEvent_t ev, hipStream_t s) { return ev ? hipEventRecord(ev, s) : hipSuccess; }
 
 // One-row items (row, len, kvoff): decode steps and ragged batches, one launch.
 hipError_t row_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s);
+// A one-row step fused with k_rope(q), k_rope(k) and the K/V append at slot a.pos (the row's
+// last visible slot): q is rotated (and left rotated), k and v (f32 [nkv][hd]) go into the
+// caches. Requires hd % 32 == 0 and, for neox pairs, rope_dim/2 % 32 == 0.
+struct RopeArgs {
+    float* q;
+    const float* k;
+    const float* v;
+    const float* inv_freq;
+    const uint32_t* positions;
+    uint32_t rope_dim, neox;
+};
+hipError_t row_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s);
+bool row_fusable(uint32_t hd, uint32_t rope_dim, uint32_t neox);
 // Multi-row items (tree rows, short lines) with chunk and nchunk set.
 hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
                             Workspace& ws, hipStream_t s);

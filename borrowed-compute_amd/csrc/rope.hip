@@ -19,13 +19,6 @@
 
 namespace bchip {
 
-__device__ __forceinline__ void rotate(float x0, float x1, float theta, float& y0, float& y1) {
-    float s, c;
-    sincosf(theta, &s, &c);
-    y0 = x0 * c - x1 * s;
-    y1 = x0 * s + x1 * c;
-}
-
 __global__ __launch_bounds__(256) void k_rope(float* __restrict__ x, const float* __restrict__ inv_freq,
                                               const uint32_t* __restrict__ positions, uint32_t rows,
                                               uint32_t heads, uint32_t hd, uint32_t rope_dim, uint32_t neox) {
@@ -44,33 +37,21 @@ __global__ __launch_bounds__(256) void k_rope(float* __restrict__ x, const float
 }
 
 template <typename KVT>
-__device__ __forceinline__ KVT to_kv(float v);
-template <>
-__device__ __forceinline__ f16 to_kv<f16>(float v) {
-    return (f16)v;
-}
-template <>
-__device__ __forceinline__ float to_kv<float>(float v) {
-    return v;
-}
-
-template <typename KVT>
 __global__ __launch_bounds__(256) void k_rope_append(float* __restrict__ q, const float* __restrict__ k,
                                                      const float* __restrict__ v, KVT* __restrict__ kc,
                                                      KVT* __restrict__ vc, const float* __restrict__ inv_freq,
                                                      const uint32_t* __restrict__ positions, uint32_t rows,
                                                      uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim,
                                                      uint32_t neox, uint64_t slot0) {
-    const uint32_t half = hd / 2, hh = rope_dim / 2, heads = nh + 2 * nkv;
+    const uint32_t half = hd / 2, heads = nh + 2 * nkv;
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (uint64_t)rows * heads * half) return;
     const uint32_t p = idx % half, hx = (idx / half) % heads;
     const uint64_t r = idx / ((uint64_t)half * heads);
     const uint64_t kvd = (uint64_t)nkv * hd;
     // Dims of this thread's pair: a rotated pair, or two dims past rope_dim.
-    const bool rot = p < hh;
-    const uint32_t a = rot ? (neox ? p : 2 * p) : rope_dim + 2 * (p - hh);
-    const uint32_t b = rot ? (neox ? p + hh : 2 * p + 1) : a + 1;
+    uint32_t a, b;
+    const bool rot = rope_pair(p, rope_dim, neox, a, b);
     if (hx < nh) {
         if (!rot) return;
         float* hp = q + (r * nh + hx) * hd;

@@ -130,6 +130,19 @@ int bchip_attention(bchip_ctx* ctx, const float* q, const void* kc, const void* 
                     uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t pos,
                     float scale);
 
+/* One decode step of one layer as a single call: bchip_rope_append with rows = 1 and
+ * slot0 = pos, then bchip_attention with rows = 1, tree = 0 at pos, with the same results
+ * bit for bit (out; q left rotated; the new row in kc and vc). It is the peephole over the
+ * five commands k_rope(q), k_rope(k), k_copy(k), k_copy(v), k_attention that
+ * Layers::forward queues per layer for a one-token pass (gpu/mod.rs:464-482): the rotation
+ * and the append run inside the attention kernel, which takes the new row from registers.
+ * Shapes the fused kernel does not take (hd % 32 != 0, or neox pairs with rope_dim/2 not a
+ * multiple of 32) run as the two calls. positions: device u32 [1]. */
+int bchip_rope_append_attention(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
+                                uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,
+                                uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos,
+                                float scale, float* out);
+
 /* Several conversations' one-token steps in one launch (the reference runs one
  * k_attention per KV stream, crates/bc-mesh/src/engine.rs:25,305-309): sequence i's row
  * q[i] [nh][hd] sees the seq_lens[i] slots kv_offsets[i] .. kv_offsets[i]+seq_lens[i]-1 of
@@ -151,6 +164,12 @@ int bchip_fill_normal(bchip_ctx* ctx, void* dst, uint32_t type, uint64_t n, uint
  * for it and returns the milliseconds between them. */
 int bchip_timer_start(bchip_ctx* ctx);
 int bchip_timer_stop(bchip_ctx* ctx, float* ms);
+/* Arms the next attention call (bchip_attention, bchip_attention_ragged,
+ * bchip_rope_append_attention) to record the caller's HIP events `before` and `after`
+ * (hipEvent_t) on the context's stream right before and right after its main attention
+ * kernel, leaving out the V^T pack before it and the fold or combine after it: the duration
+ * of the dominant kernel as a kernel trace reports it. One call consumes the arming. */
+int bchip_timer_arm(bchip_ctx* ctx, void* before, void* after);
 
 #ifdef __cplusplus
 }
