@@ -31,6 +31,7 @@
 #include "common.hpp"
 #include "internal.hpp"
 
+#include <hip/hip_ext.h>
 #include <math.h>
 #include <type_traits>
 #include <stdlib.h>
@@ -1424,8 +1425,8 @@ static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream
 }
 
 template <int HD, typename KVT, int W, int NT>
-static hipError_t launch_shared_t(const SharedParams& sp, uint32_t blocks, hipStream_t s) {
-    hipLaunchKernelGGL((attn_shared<HD, KVT, W, NT>), dim3(blocks), dim3(64 * W), 0, s, sp);
+static hipError_t launch_shared_t(const SharedParams& sp, uint32_t blocks, const AttnCall& a, hipStream_t s) {
+    hipExtLaunchKernelGGL((attn_shared<HD, KVT, W, NT>), dim3(blocks), dim3(64 * W), 0, s, a.ev_before, a.ev_after, 0, sp);
     return hipGetLastError();
 }
 
@@ -1450,28 +1451,23 @@ static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream
 template <int HD, typename KVT>
 static hipError_t launch_decode_t(DirectParams& dp, CombineParams& cp, const AttnCall& a, hipStream_t s) {
     const dim3 block(256);
-    hipError_t e = mark(a.ev_before, s);
-    if (e != hipSuccess) return e;
     if (dp.tree)
-        hipLaunchKernelGGL((attn_decode<HD, KVT, true>), dim3(dp.nunits), block, 0, s, dp);
+        hipExtLaunchKernelGGL((attn_decode<HD, KVT, true>), dim3(dp.nunits), block, 0, s, a.ev_before, a.ev_after, 0, dp);
     else
-        hipLaunchKernelGGL((attn_decode<HD, KVT, false>), dim3(dp.nunits), block, 0, s, dp);
-    e = hipGetLastError();
-    if (e == hipSuccess) e = mark(a.ev_after, s);
+        hipExtLaunchKernelGGL((attn_decode<HD, KVT, false>), dim3(dp.nunits), block, 0, s, a.ev_before, a.ev_after, 0, dp);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_combine_t<HD>(cp, dp.nitems * dp.nkv, s);
 }
 
 template <int HD, typename KVT>
 static hipError_t launch_row_t(const DirectParams& dp, bool fold, const AttnCall& a, hipStream_t s) {
-    hipError_t e = mark(a.ev_before, s);
-    if (e != hipSuccess) return e;
+    const dim3 grid(ceil_div(dp.nunits, 4)), block(256);
     if (dp.fuse)
-        hipLaunchKernelGGL((attn_decode_row<HD, KVT, true>), dim3(ceil_div(dp.nunits, 4)), dim3(256), 0, s, dp);
+        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, true>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
     else
-        hipLaunchKernelGGL((attn_decode_row<HD, KVT, false>), dim3(ceil_div(dp.nunits, 4)), dim3(256), 0, s, dp);
-    e = hipGetLastError();
-    if (e == hipSuccess) e = mark(a.ev_after, s);
+        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, false>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess || !fold) return e;
     hipLaunchKernelGGL((attn_row_fold<HD>), dim3(dp.nitems * dp.nkv * dp.G), dim3(256), 0, s, dp);
     return hipGetLastError();
@@ -1666,36 +1662,28 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
             hipLaunchKernelGGL(vt_pack, dim3(nb, a.nkv), dim3(256), 0, s, (const f16*)a.vc,
                                (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, sp.vt_npad);
             e = hipGetLastError();
-            if (e == hipSuccess) e = mark(a.ev_before, s);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((attn_prefill<8, true, 4>), dim3(blocks), dim3(512), 0, s, sp);
+            hipExtLaunchKernelGGL((attn_prefill<8, true, 4>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
+        } else if (wide) {
+            hipExtLaunchKernelGGL((attn_prefill<8, false, 4>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else {
-            e = mark(a.ev_before, s);
-            if (e != hipSuccess) return e;
-            if (wide)
-                hipLaunchKernelGGL((attn_prefill<8, false, 4>), dim3(blocks), dim3(512), 0, s, sp);
-            else
-                hipLaunchKernelGGL((attn_prefill<4, false, 4>), dim3(blocks), dim3(256), 0, s, sp);
+            hipExtLaunchKernelGGL((attn_prefill<4, false, 4>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
         }
         e = hipGetLastError();
-        if (e == hipSuccess) e = mark(a.ev_after, s);
     } else {
-        e = mark(a.ev_before, s);
-        if (e != hipSuccess) return e;
         if (a.kv_type == 1) {
             if (wide) {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, s)));
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, a, s)));
             } else {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, 1>(sp, blocks, s)));
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, 1>(sp, blocks, a, s)));
             }
         } else {
             if (wide) {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, s)));
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, a, s)));
             } else {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, 1>(sp, blocks, s)));
+                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, 1>(sp, blocks, a, s)));
             }
         }
-        if (e == hipSuccess) e = mark(a.ev_after, s);
     }
     if (e != hipSuccess || !sp.split) return e;
     CombineParams cp{};

@@ -36,13 +36,11 @@ struct AttnCall {
     uint32_t tree, rows, nh, nkv, hd, pos;
     float scale;
     uint64_t slot_limit;  // slots both caches hold (all slots a call may read when unknown)
-    // Timing: when set, recorded on the stream right before and right after the call's main
-    // attention kernel (not the V^T pack before it nor the fold or combine after it).
+    // Timing: when set, recorded at the start and the end of the call's main attention
+    // kernel by its dispatch (hipExtLaunchKernel), not the V^T pack before it nor the fold
+    // or combine after it.
     hipEvent_t ev_before = nullptr, ev_after = nullptr;
 };
-
-// Records ev on s when it is set (the calls' timing marks).
-inline hipError_t mark(hipEvent_t ev, hipStream_t s) { return ev ? hipEventRecord(ev, s) : hipSuccess; }
 
 // One-row items (row, len, kvoff): decode steps and ragged batches, one launch.
 hipError_t row_attention(const AttnCall& a, const Item* items, uint32_t nitems, Workspace& ws, hipStream_t s);

@@ -166,9 +166,10 @@ int bchip_timer_start(bchip_ctx* ctx);
 int bchip_timer_stop(bchip_ctx* ctx, float* ms);
 /* Arms the next attention call (bchip_attention, bchip_attention_ragged,
  * bchip_rope_append_attention) to record the caller's HIP events `before` and `after`
- * (hipEvent_t) on the context's stream right before and right after its main attention
- * kernel, leaving out the V^T pack before it and the fold or combine after it: the duration
- * of the dominant kernel as a kernel trace reports it. One call consumes the arming. */
+ * (hipEvent_t) at the start and the end of its main attention kernel, by that kernel's
+ * dispatch (hipExtLaunchKernel), leaving out the V^T pack before it and the fold or combine
+ * after it: the duration of the dominant kernel as a kernel trace reports it. One call
+ * consumes the arming. */
 int bchip_timer_arm(bchip_ctx* ctx, void* before, void* after);
 
 #ifdef __cplusplus
