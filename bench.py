@@ -328,7 +328,7 @@ def profiled_traffic(ctx_len):
     summary: FETCH_SIZE and WRITE_SIZE passes of rocprofv3 over this script, scaled by the
     same counters' reading for a copy of known size. None when the summary is absent or was
     taken at another context length."""
-    path = os.path.join(ROOT, "profiles", "attn_decode_llama8b_32k.txt")
+    path = os.path.join(ROOT, "profiles", "attn_decode_row_llama8b_32k.txt")
     if ctx_len != 32768 or not os.path.exists(path):
         return None
     for line in open(path):
@@ -423,7 +423,7 @@ def main():
                    "ctx": args.ctx, "layers": 32},
         "roofline": {"bound": "hbm", "achieved": head["attn_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": head["hbm_frac"], "traffic": profiled_traffic(args.ctx),
-                     "traffic_source": "profiles/attn_decode_llama8b_32k.txt (rocprofv3 FETCH_SIZE x 2.0 + "
+                     "traffic_source": "profiles/attn_decode_row_llama8b_32k.txt (rocprofv3 FETCH_SIZE x 2.0 + "
                                        "WRITE_SIZE x 1.0, factors from a 256 MiB copy)",
                      "kernel": "attn_decode_row<128, f16, fused> (bchip_rope_append_attention's attention kernel)",
                      "bytes_per_launch": head["attn_bytes_per_launch"], "launch_us": head["attn_kernel_us"],

@@ -121,10 +121,10 @@ int bchip_rope_append(bchip_ctx* ctx, float* q, const float* k, const float* v, 
  * Every row of a multi-row call (rows >= 2) is computed by the same fixed-order
  * arithmetic, which depends only on the row's q and its visible slot list: results are
  * identical whatever the batch, the row's index, or whether it is a tree node or a line
- * token. A one-row call (a decode step) cuts its list into at most 256 power-of-two chunks
- * (the count set by the list length and nkv alone), and combines the chunk states by a
- * fixed binary tree over the chunk index: deterministic, and within rounding of the same
- * row in a batch (the reference allows 1e-4, model.rs:641-642). */
+ * token. A one-row call (a decode step) cuts its list into at most 256 chunks (their length
+ * set by the list length and nkv alone) and folds the chunk states in a fixed order:
+ * deterministic, and within rounding of the same row in a batch (the reference allows
+ * 1e-4, model.rs:641-642). */
 int bchip_attention(bchip_ctx* ctx, const float* q, const void* kc, const void* vc,
                     uint32_t kv_type, float* out, const uint32_t* masks, uint32_t tree,
                     uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t pos,
