@@ -357,7 +357,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build runs on one GPU; the attention path's "
-                                   "multi-GPU sharding is described in DESIGN.md, not run"}))
+                                   "split over several GPUs (by KV head or by sequence chunk) is a design, not run here"}))
         sys.exit(2)
     want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "ragged", "calib", "cpu"}
     hip = Hip()

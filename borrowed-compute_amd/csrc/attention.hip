@@ -534,8 +534,10 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 // entries, with no barrier and no exchange between waves. Lane (n, g) holds slot n (query
 // head kvh * G + n) of keys 4g..4g+3 of each 16-key tile; the block's max and sum cross the
 // four lane groups by permlane swaps, which hand every lane the pair (x[l], x[l^16]) or
-// (x[l], x[l^32]) in the same order. V goes through the wave's own LDS rows and comes back
-// transposed. The four waves of a workgroup take consecutive units, four KV heads of one
+// (x[l], x[l^32]) in the same order. K and V go through the wave's own LDS rows (loaded
+// row-contiguous), K comes back in the score operands' layout and V transposed. The list's
+// last entry (a fused step's new row) is a block of its own at the end of the last chunk.
+// The four waves of a workgroup take consecutive units, four KV heads of one
 // chunk, so a workgroup reads 4 * hd contiguous elements of every row it streams (measured
 // faster than four chunks of one head: 25.5 against 30.9 us at 32768 slots x 8 KV heads).
 // A unit whose chunk is the whole list writes the output; otherwise its state goes to the
@@ -544,6 +546,7 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 // takes a device-scope release, an L2 write-back per workgroup: measured at +8 us for 256
 // workgroups and +175 us for 4096 on MI355X.)
 constexpr int RB = 32;                     // list entries per block of the one-row kernel
+constexpr uint32_t ROW_FUSE_MAXG = 8;      // query heads per KV head a fused step takes
 constexpr uint32_t ROW_MAX_CHUNKS = 256;   // chunks per (item, KV head): attn_row_fold's reach
 constexpr uint32_t ROW_FOLD_BATCH = 16;    // chunk states a thread loads before folding them
 
@@ -556,159 +559,250 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     constexpr int VRI = 64 / VLR;       // V rows per load
     constexpr int NVL = RB / VRI;       // V loads per block
     __shared__ __attribute__((aligned(16))) f16 vl[4][RB * VS];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // K through LDS where it fits beside V (f16, hd <= 128): K then loads as V does, 16 lanes
+    // over a row's contiguous bytes, and the score operands come from the LDS tile (measured
+    // faster than loading the operands straight into registers, 16 rows by 64 bytes a load:
+    // 25.9 against 28.0 us at 32768 slots x 8 KV heads, and 131 against 154 us for the
+    // ragged batch).
+    constexpr bool KL = sizeof(KVT) == 2 && HD <= 128;
+    constexpr int KS = HD + 8;  // LDS row stride of K (halves): rows 4 banks apart
+    __shared__ __attribute__((aligned(16))) f16 kt[KL ? 4 : 1][KL ? RB * KS : 8];
+    // The list's last entry (a fused step's new row) as the cache holds it, per wave: K then
+    // V, dims past hd zero. The chunk that holds it takes it as a block of its own, after
+    // its other entries, from here.
+    __shared__ __attribute__((aligned(16))) KVT lrow[4][2][HD];
+    // The wave index is uniform: every bound derived from it below (the unit, its chunk and
+    // KV head, the block loop's end) stays in scalar registers, so the loop's exit is a
+    // scalar branch and the loads of the next block need not wait for those in flight.
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, n = lane & 15;
     const uint32_t u = blockIdx.x * 4u + w;  // this wave's unit
     if (u >= p.nunits) return;               // no barrier below: a wave may leave alone
     uint32_t it = 0;
     while (it + 1 < p.nitems && u >= p.items[it + 1].unit0) it++;
     const Item I = p.items[it];
+    const uint32_t pos0 = FUSE ? p.positions[0] : 0u;  // before any store: a scalar load
     const uint32_t hd = p.hd, kvd = p.nkv * hd, G = p.G;
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = rem % p.nkv;
     const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, I.len);
+    // The last chunk streams up to the list's last entry and then takes that entry alone:
+    // the same blocks whether the entry came from the cache or, in a fused step, from
+    // registers (so both give the same bits), and no block of the stream holds a slot this
+    // kernel writes.
+    const uint32_t last = I.len - 1;
+    const bool has_last = kb1 == I.len;
+    const uint32_t kbs = has_last ? last : kb1;  // end of the streamed entries
     const bool valid = (uint32_t)n < G;
     const KVT* zp = (const KVT*)p.zero;
     const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
     const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
 
-    // Block key0 into registers; entries at or past kb1 read the zero page (no HBM traffic,
+    // Block key0 into registers; entries at or past kbs read the zero page (no HBM traffic,
     // no branch between the loads).
-    auto load_block = [&](uint32_t key0, Raw<KVT> (&kr)[2][NKC], Raw<KVT> (&vr)[NVL]) {
+    auto load_k = [&](uint32_t key0, Raw<KVT> (&kr)[2][NKC]) {
+        if constexpr (KL) {
+            // Row-contiguous: load i holds entry key0 + i VRI + lane / VLR, dims 8 (lane % VLR).
+            const uint32_t d = 8 * (lane % VLR);
+#pragma unroll
+            for (int i = 0; i < NVL; i++) {
+                const uint32_t key = key0 + i * VRI + lane / VLR;
+                kr[i / NKC][i % NKC].load_stream((key < kbs && d < hd) ? kc + (size_t)key * kvd + d : zp);
+            }
+            return;
+        }
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const uint32_t key = key0 + 16 * t + n;
-            const KVT* row = kc + (size_t)(key < kb1 ? key : 0u) * kvd;
+            const KVT* row = kc + (size_t)(key < kbs ? key : 0u) * kvd;
 #pragma unroll
             for (int c2 = 0; c2 < NKC; c2++) {
                 const uint32_t hd0 = 32 * c2 + 8 * g;
-                kr[t][c2].load_stream((key < kb1 && hd0 < hd) ? row + hd0 : zp);
+                kr[t][c2].load_stream((key < kbs && hd0 < hd) ? row + hd0 : zp);
             }
         }
+    };
+    auto load_v = [&](uint32_t key0, Raw<KVT> (&vr)[NVL]) {
         const uint32_t d = 8 * (lane % VLR);
 #pragma unroll
         for (int i = 0; i < NVL; i++) {
             const uint32_t key = key0 + i * VRI + lane / VLR;
-            vr[i].load_stream((key < kb1 && d < hd) ? vc + (size_t)key * kvd + d : zp);
+            vr[i].load_stream((key < kbs && d < hd) ? vc + (size_t)key * kvd + d : zp);
         }
     };
-    // Q^T operands (B of the score MFMAs), straight into registers; fused with RoPE, the
-    // wave first rotates its G heads into its LDS tile, one pair per lane, and takes the
-    // operands from there.
-    half8 qb[NKC];
+    // Prologue. Every small load (q, the RoPE frequencies, the new or the last K/V row) goes
+    // out before the first blocks' loads, unconditionally (lanes with nothing to read load
+    // the zero page): a wave's loads complete in issue order, and a load behind a branch
+    // makes the compiler wait for all loads in flight where the branch joins. The rotation
+    // of a fused step then runs while the blocks are in flight.
+    half8 qb[NKC];  // Q^T operands (B of the score MFMAs)
     f16* vw = vl[w];
-    const uint32_t newslot = I.len - 1;
-    const bool has_new = FUSE && newslot >= kb0 && newslot < kb1;  // this chunk holds the new row
-    Raw<KVT> kn[NKC], vn;  // the new row's K operands and V elements, as the cache holds them
-    // The first block's loads go out before anything else (double-buffered path).
+    const bool has_new = FUSE && has_last;  // this chunk writes the new row
     constexpr bool DB = sizeof(KVT) == 2 && HD <= 128;
-    Raw<KVT> kA[2][NKC], vA[NVL], kB[2][NKC], vB[NVL];
-    if constexpr (DB) load_block(kb0, kA, vA);
+    constexpr int NLE = (HD + 63) / 64;                              // row elements per lane
+    constexpr int NPJ = (HD / 2 + 63) / 64;                          // RoPE pairs per lane
+    constexpr int NQL = FUSE ? ((int)ROW_FUSE_MAXG * HD + 255) / 256 : 1;  // q float4s per lane
+    const uint32_t half = hd / 2;
+    const float* zf = (const float*)p.zero;
+    KVT lk[NLE], lv[NLE];     // !FUSE: the last entry, from the cache
+    float4 qa[NKC], qc[NKC];  // !FUSE: q
+    float fr[NPJ];            // FUSE: frequencies of this lane's pairs
+    // FUSE: the G heads' q (qs [G][hd] in the wave's LDS tile), the new k (ks) and v (vs),
+    // 16 bytes a lane per load; the rotation works in LDS.
+    float* qs = (float*)vw;
+    float* ks = qs + NQL * 256;
+    float* vs = ks + 256;
+    static_assert(!FUSE || (NQL * 256 + 512) * 4 <= RB * VS * 2, "the fused prologue's q, k, v fit the wave's tile");
+    f32x4 qf[NQL], kf, vf;
     if constexpr (FUSE) {
-        float* qs = (float*)vw;  // [G][HD] rotated q, then [HD] rotated k of the new row
-        // Lane pairs pp = lane + 64j: the angle depends on the pair alone, so its sine and
-        // cosine serve all G heads and the new K row.
-        constexpr int NPJ = (HD / 2 + 63) / 64;
-        const float posf = (float)p.positions[0];
-        const uint32_t half = hd / 2;
-        float sn[NPJ], cs[NPJ];
-        uint32_t pa[NPJ], pb[NPJ];
-        bool prot[NPJ];
 #pragma unroll
         for (int j = 0; j < NPJ; j++) {
             const uint32_t pp = lane + 64 * j;
-            prot[j] = pp < half && rope_pair(pp, p.rope_dim, p.neox, pa[j], pb[j]);
-            if (pp >= half) pa[j] = pb[j] = 0;
-            sn[j] = 0.0f;
-            cs[j] = 1.0f;
-            if (prot[j]) sincosf(posf * p.inv_freq[pp], &sn[j], &cs[j]);
+            fr[j] = *(pp < p.rope_dim / 2 ? p.inv_freq + pp : zf);
         }
-        for (uint32_t h = 0; h < G; h++) {
-            const float* qr = p.q + ((size_t)I.row * p.nh + kvh * G + h) * hd;
+        const float* qg = p.q + ((size_t)I.row * p.nh + kvh * G) * hd;
 #pragma unroll
-            for (int j = 0; j < NPJ; j++) {
-                if (lane + 64 * j >= half) continue;
-                float y0 = qr[pa[j]], y1 = qr[pb[j]];
-                if (prot[j]) rotate_sc(qr[pa[j]], qr[pb[j]], sn[j], cs[j], y0, y1);
-                qs[h * HD + pa[j]] = y0;
-                qs[h * HD + pb[j]] = y1;
+        for (int i = 0; i < NQL; i++) {
+            const uint32_t e = 4 * (lane + 64 * i);
+            qf[i] = *(const f32x4*)(e < G * hd ? qg + e : zf);
+        }
+        const bool nk = has_new && 4 * (uint32_t)lane < hd;
+        kf = *(const f32x4*)(nk ? p.knew + (size_t)kvh * hd + 4 * lane : zf);
+        vf = *(const f32x4*)(nk ? p.vnew + (size_t)kvh * hd + 4 * lane : zf);
+    } else {
+#pragma unroll
+        for (int j = 0; j < NLE; j++) {
+            const uint32_t e = lane + 64 * j;
+            const bool ok = has_last && e < hd;
+            lk[j] = *(ok ? kc + (size_t)last * kvd + e : zp);
+            lv[j] = *(ok ? vc + (size_t)last * kvd + e : zp);
+        }
+        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * G + (valid ? n : 0)) * hd;
+#pragma unroll
+        for (int c2 = 0; c2 < NKC; c2++) {
+            const uint32_t hd0 = 32 * c2 + 8 * g;
+            const float* src = (valid && hd0 < hd) ? qrow + hd0 : zf;
+            qa[c2] = *(const float4*)src;
+            qc[c2] = *(const float4*)(src + 4);
+        }
+    }
+    Raw<KVT> kR[2][2][NKC], vR[NVL];
+    if constexpr (DB) {
+        // The first block, and the second block's K: in flight through the prologue (the
+        // wait for q, the rotation of a fused step).
+        load_k(kb0, kR[0]);
+        load_v(kb0, vR);
+        load_k(kb0 + RB, kR[1]);
+    }
+    if constexpr (FUSE) {
+        // q, k and v into the LDS tile; then each lane rotates its pairs there (the angle
+        // depends on the pair alone, so its sine and cosine serve all G heads and the new K
+        // row), and the operands come from there.
+#pragma unroll
+        for (int i = 0; i < NQL; i++) *(f32x4*)&qs[4 * (lane + 64 * i)] = qf[i];
+        *(f32x4*)&ks[4 * lane] = kf;
+        *(f32x4*)&vs[4 * lane] = vf;
+        const float posf = (float)pos0;
+#pragma unroll
+        for (int j = 0; j < NPJ; j++) {
+            const uint32_t pp = lane + 64 * j;
+            if (pp >= half) continue;
+            uint32_t a, b;
+            const bool rot = rope_pair(pp, p.rope_dim, p.neox, a, b);
+            float sn = 0.0f, cs = 1.0f;
+            if (rot) sincosf(posf * fr[j], &sn, &cs);
+            for (uint32_t h = 0; h < G; h++) {
+                float y0 = qs[h * hd + a], y1 = qs[h * hd + b];
+                if (rot) rotate_sc(qs[h * hd + a], qs[h * hd + b], sn, cs, y0, y1);
+                qs[h * hd + a] = y0;
+                qs[h * hd + b] = y1;
+            }
+            if (has_new) {
+                float y0 = ks[a], y1 = ks[b];
+                if (rot) rotate_sc(ks[a], ks[b], sn, cs, y0, y1);
+                const KVT k0 = to_kv<KVT>(y0), k1 = to_kv<KVT>(y1);
+                KVT* kdst = (KVT*)p.kc + (I.kvoff + last) * kvd + (size_t)kvh * hd;
+                kdst[a] = k0;
+                kdst[b] = k1;
+                lrow[w][0][a] = k0;
+                lrow[w][0][b] = k1;
             }
         }
         if (has_new) {
-            const float* kr = p.knew + (size_t)kvh * hd;
-            KVT* kdst = (KVT*)p.kc + (I.kvoff + newslot) * kvd + (size_t)kvh * hd;
-#pragma unroll
-            for (int j = 0; j < NPJ; j++) {
-                if (lane + 64 * j >= half) continue;
-                float y0 = kr[pa[j]], y1 = kr[pb[j]];
-                if (prot[j]) rotate_sc(kr[pa[j]], kr[pb[j]], sn[j], cs[j], y0, y1);
-                qs[G * HD + pa[j]] = y0;
-                qs[G * HD + pb[j]] = y1;
-                kdst[pa[j]] = to_kv<KVT>(y0);
-                kdst[pb[j]] = to_kv<KVT>(y1);
+            // V as the cache holds it, and zeros past hd in both rows.
+            const uint32_t e = 4 * lane;
+            if (e < (uint32_t)HD) {
+                const KVT v0 = to_kv<KVT>(vs[e]), v1 = to_kv<KVT>(vs[e + 1]), v2 = to_kv<KVT>(vs[e + 2]),
+                          v3 = to_kv<KVT>(vs[e + 3]);
+                if (e < hd) {
+                    KVT* vdst = (KVT*)p.vc + (I.kvoff + last) * kvd + (size_t)kvh * hd + e;
+                    vdst[0] = v0;
+                    vdst[1] = v1;
+                    vdst[2] = v2;
+                    vdst[3] = v3;
+                } else {
+                    lrow[w][0][e] = lrow[w][0][e + 1] = lrow[w][0][e + 2] = lrow[w][0][e + 3] = to_kv<KVT>(0.0f);
+                }
+                lrow[w][1][e] = v0;
+                lrow[w][1][e + 1] = v1;
+                lrow[w][1][e + 2] = v2;
+                lrow[w][1][e + 3] = v3;
             }
-            const float* vr = p.vnew + (size_t)kvh * hd;
-            KVT* vdst = (KVT*)p.vc + (I.kvoff + newslot) * kvd + (size_t)kvh * hd;
-            for (uint32_t e = lane; e < hd; e += 64) vdst[e] = to_kv<KVT>(vr[e]);
-            const float4 z = float4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int c2 = 0; c2 < NKC; c2++) {
-                const uint32_t hd0 = 32 * c2 + 8 * g;
-                kn[c2].set(hd0 < hd ? *(const float4*)&qs[G * HD + hd0] : z, hd0 < hd ? *(const float4*)&qs[G * HD + hd0 + 4] : z);
-            }
-            const uint32_t d = 8 * (lane % VLR);
-            vn.set(d < hd ? *(const float4*)(vr + d) : z, d < hd ? *(const float4*)(vr + d + 4) : z);
         }
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++) {
             const uint32_t hd0 = 32 * c2 + 8 * g;
             const bool ok = valid && hd0 < hd;
             const float4 z = float4{0.0f, 0.0f, 0.0f, 0.0f};
-            qb[c2] = q_scaled(ok ? *(const float4*)&qs[n * HD + hd0] : z, ok ? *(const float4*)&qs[n * HD + hd0 + 4] : z, p.sc);
+            qb[c2] = q_scaled(ok ? *(const float4*)&qs[n * hd + hd0] : z, ok ? *(const float4*)&qs[n * hd + hd0 + 4] : z, p.sc);
         }
         // q stays rotated, as k_rope leaves it. Other units of this KV head may still be
         // reading it, so with several chunks the first one stages the rotated heads and
         // attn_row_fold, which runs after every unit, copies them into q; a lone unit writes q.
         if (c == 0) {
             float* dst = I.nchunk == 1 ? p.qw + (size_t)I.row * p.nh * hd : p.qrot;
-            for (uint32_t e = lane; e < G * hd; e += 64) {
-                const uint32_t h = e / hd, d = e % hd;
-                dst[(size_t)(kvh * G + h) * hd + d] = qs[h * HD + d];
-            }
+            for (uint32_t e = lane; e < G * hd; e += 64) dst[(size_t)kvh * G * hd + e] = qs[e];
         }
     } else {
-        const float* qrow = p.q + ((size_t)I.row * p.nh + kvh * G + (valid ? n : 0)) * hd;
-        float4 qa[NKC], qc[NKC];
-#pragma unroll
-        for (int c2 = 0; c2 < NKC; c2++) {
-            const uint32_t hd0 = 32 * c2 + 8 * g;
-            const float* src = (valid && hd0 < hd) ? qrow + hd0 : (const float*)p.zero;
-            qa[c2] = *(const float4*)src;
-            qc[c2] = *(const float4*)(src + 4);
-        }
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++) qb[c2] = q_scaled(qa[c2], qc[c2], p.sc);
+        if (has_last) {
+#pragma unroll
+            for (int j = 0; j < NLE; j++) {
+                const uint32_t e = lane + 64 * j;
+                if (e < (uint32_t)HD) {
+                    lrow[w][0][e] = lk[j];
+                    lrow[w][1][e] = lv[j];
+                }
+            }
+        }
     }
     f32x4 o[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
-    // SUB: the block holding the new row (fused steps), whose lanes on that row take kn, vn
-    // in place of what they loaded.
-    auto compute_block = [&](uint32_t key0, const Raw<KVT> (&kr)[2][NKC], const Raw<KVT> (&vr)[NVL], auto SUB) {
-        constexpr bool sub = decltype(SUB)::value;
-#pragma unroll
-        for (int i = 0; i < NVL; i++) {
-            half8 v = vr[i].get();
-            if constexpr (sub) v = (key0 + i * VRI + lane / VLR == newslot) ? vn.get() : v;
-            v_store<VS>(vw, i * VRI + lane / VLR, 8 * (lane % VLR), v);
-        }
+    // One block of RB entries from key0; entries at or past `end` are masked. after_v runs
+    // once the block's V is in LDS (its registers free), before the PV products.
+    auto compute_block = [&](uint32_t key0, uint32_t end, const Raw<KVT> (&kr)[2][NKC], const Raw<KVT> (&vr)[NVL],
+                             auto after_v) {
         f32x4 st[2];
+        if constexpr (KL) {
+            f16* kw = kt[KL ? w : 0];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            const bool mine = sub && key0 + 16 * t + n == newslot;
+            for (int i = 0; i < NVL; i++) *(half8*)&kw[(i * VRI + lane / VLR) * KS + 8 * (lane % VLR)] = kr[i / NKC][i % NKC].get();
 #pragma unroll
-            for (int c2 = 0; c2 < NKC; c2++) st[t] = mfma16(mine ? kn[c2].get() : kr[t][c2].get(), qb[c2], st[t]);
+            for (int t = 0; t < 2; t++) {
+                st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int c2 = 0; c2 < NKC; c2++)
+                    st[t] = mfma16(*(const half8*)&kw[(16 * t + n) * KS + 32 * c2 + 8 * g], qb[c2], st[t]);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int c2 = 0; c2 < NKC; c2++) st[t] = mfma16(kr[t][c2].get(), qb[c2], st[t]);
+            }
         }
         float x[2][4], mx = -INFINITY;
 #pragma unroll
@@ -716,7 +810,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t k = key0 + 16 * t + 4 * g + i;
-                x[t][i] = (k < kb1) ? st[t][i] : -INFINITY;
+                x[t][i] = (k < end) ? st[t][i] : -INFINITY;
                 mx = fmaxf(mx, x[t][i]);
             }
         mx = xmax32(xmax16(mx));
@@ -735,35 +829,62 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         ts = xsum32(xsum16(ts));
         l = l * corr + ts;
         m = mn;
+#pragma unroll
+        for (int i = 0; i < NVL; i++) v_store<VS>(vw, i * VRI + lane / VLR, 8 * (lane % VLR), vr[i].get());
+        after_v();
         rescale(o, corr);
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) o[dt] = mfma16(v_operand<VS>(vw, dt, 0, g, n), pb, o[dt]);
     };
-    // Two register sets in turn where they fit (f16, hd <= 128): the next block loads while
-    // this one computes. Wider rows load and compute one block at a time; the other resident
-    // waves of the CU still overlap them.
-    auto compute = [&](uint32_t key0, const Raw<KVT> (&kr)[2][NKC], const Raw<KVT> (&vr)[NVL]) {
-        if (FUSE && has_new && newslot - key0 < (uint32_t)RB)
-            compute_block(key0, kr, vr, std::integral_constant<bool, FUSE>{});
-        else
-            compute_block(key0, kr, vr, std::false_type{});
-    };
+    auto nothing = [] {};
+    // Where two K register sets fit (f16, hd <= 128), the loads run one block ahead in halves:
+    // the next block's K goes out before this block's scores, its V once this block's V is in
+    // LDS. About one block per wave is in flight at any time, beside the compute; a deeper
+    // prefetch measured slower (more requests in flight than the memory system serves
+    // best). Wider rows load and compute one block at a time; the other resident waves of
+    // the CU still overlap them.
     if constexpr (DB) {
-        for (uint32_t key0 = kb0;;) {
-            load_block(key0 + RB, kB, vB);
-            compute(key0, kA, vA);
-            key0 += RB;
-            if (key0 >= kb1) break;
-            load_block(key0 + RB, kA, vA);
-            compute(key0, kB, vB);
-            key0 += RB;
-            if (key0 >= kb1) break;
+        // The first block, then two blocks per trip and one exit, at the bottom: with an exit
+        // after every block the compiler merges the exits into one block that also leads back
+        // to the loop's top, and must then assume loads of every register set are still in
+        // flight there. A chunk with an even block count computes one block past its end: its
+        // entries are all masked (P = 0 exactly, the max and the scale hold), its loads read
+        // the zero page, and the state comes out unchanged.
+        compute_block(kb0, kbs, kR[0], vR, [&] { load_v(kb0 + RB, vR); });
+        for (uint32_t key0 = kb0 + RB; key0 < kbs; key0 += 2 * RB) {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const uint32_t kb = key0 + s * RB;
+                load_k(kb + RB, kR[s]);
+                compute_block(kb, kbs, kR[1 - s], vR, [&] { load_v(kb + RB, vR); });
+            }
         }
     } else {
-        for (uint32_t key0 = kb0; key0 < kb1; key0 += RB) {
-            load_block(key0, kA, vA);
-            compute(key0, kA, vA);
+        for (uint32_t key0 = kb0; key0 < kbs; key0 += RB) {
+            load_k(key0, kR[0]);
+            load_v(key0, vR);
+            compute_block(key0, kbs, kR[0], vR, nothing);
         }
+    }
+    if (has_last) {
+        // The last entry as a block of its own: every K row of the block is that entry (the
+        // rows past it are masked), V rows past it are zero.
+        Raw<KVT> kx[2][NKC], vx[NVL];
+        if constexpr (KL) {
+#pragma unroll
+            for (int i = 0; i < NVL; i++) kx[i / NKC][i % NKC].load(&lrow[w][0][8 * (lane % VLR)]);
+        } else {
+#pragma unroll
+            for (int c2 = 0; c2 < NKC; c2++) {
+                kx[0][c2].load(&lrow[w][0][32 * c2 + 8 * g]);
+                kx[1][c2] = kx[0][c2];
+            }
+        }
+        vx[0].load(&lrow[w][1][8 * (lane % VLR)]);
+        if (lane >= VLR) vx[0].set(float4{0.0f, 0.0f, 0.0f, 0.0f}, float4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+        for (int i = 1; i < NVL; i++) vx[i].set(float4{0.0f, 0.0f, 0.0f, 0.0f}, float4{0.0f, 0.0f, 0.0f, 0.0f});
+        compute_block(last, I.len, kx, vx, nothing);
     }
     if (!valid) return;
     if (I.nchunk == 1) {
@@ -1509,9 +1630,12 @@ uint32_t row_chunk(uint64_t len, uint32_t nkv) {
     return (uint32_t)std::max<uint64_t>(chunk, 2 * RB);
 }
 
-bool row_fusable(uint32_t hd, uint32_t rope_dim, uint32_t neox) {
-    // Every rotated pair's two dims sit in one lane's operand groups (dims 32c + 8g + j).
-    return hd % 32 == 0 && hd <= MAX_HD && rope_dim % 2 == 0 && rope_dim <= hd && (!neox || (rope_dim / 2) % 32 == 0);
+bool row_fusable(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox) {
+    // The shapes the fused kernel is built and tested for: whole 32-dim operand groups, neox
+    // halves of whole groups, and at most ROW_FUSE_MAXG query heads per KV head (each lane
+    // holds its pairs of every head of the group in registers); others run as the two calls.
+    return nkv > 0 && nh % nkv == 0 && nh / nkv <= ROW_FUSE_MAXG && hd % 32 == 0 && hd <= MAX_HD &&
+           rope_dim % 2 == 0 && rope_dim <= hd && (!neox || (rope_dim / 2) % 32 == 0);
 }
 
 static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nitems, const RopeArgs* rope,
@@ -1522,7 +1646,7 @@ hipError_t row_attention(const AttnCall& a, const Item* items, uint32_t nitems, 
 }
 
 hipError_t row_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s) {
-    if (!row_fusable(a.hd, r.rope_dim, r.neox)) return hipErrorInvalidValue;
+    if (!row_fusable(a.nh, a.nkv, a.hd, r.rope_dim, r.neox)) return hipErrorInvalidValue;
     Item item{};
     item.row = 0;
     item.nrows = 1;

@@ -454,7 +454,7 @@ int bchip_rope_append_attention(bchip_ctx* c, float* q, const float* k, const fl
     if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
     CHECK(check_heads(nh, nkv, hd));
     if (rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
-    if (!row_fusable(hd, rope_dim, neox)) {
+    if (!row_fusable(nh, nkv, hd, rope_dim, neox)) {
         CHECK(bchip_rope_append(c, q, k, v, kc, vc, kv_type, inv_freq, positions, 1, nh, nkv, hd, rope_dim, neox, pos));
         return bchip_attention(c, q, kc, vc, kv_type, out, nullptr, 0, 1, nh, nkv, hd, pos, scale);
     }
