@@ -641,6 +641,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     constexpr int NLE = (HD + 63) / 64;                              // row elements per lane
     constexpr int NPJ = (HD / 2 + 63) / 64;                          // RoPE pairs per lane
     constexpr int NQL = FUSE ? ((int)ROW_FUSE_MAXG * HD + 255) / 256 : 1;  // q float4s per lane
+    constexpr int MG = FUSE ? (int)ROW_FUSE_MAXG : 1;
     const uint32_t half = hd / 2;
     const float* zf = (const float*)p.zero;
     KVT lk[NLE], lv[NLE];     // !FUSE: the last entry, from the cache
@@ -702,21 +703,33 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         *(f32x4*)&ks[4 * lane] = kf;
         *(f32x4*)&vs[4 * lane] = vf;
         const float posf = (float)pos0;
+        // All ROW_FUSE_MAXG heads' pairs at once (heads past G are the zeros their loads
+        // read), so the LDS reads go out together; unrotated dims pass through unchanged.
 #pragma unroll
         for (int j = 0; j < NPJ; j++) {
             const uint32_t pp = lane + 64 * j;
-            if (pp >= half) continue;
+            const bool act = pp < half;
             uint32_t a, b;
-            const bool rot = rope_pair(pp, p.rope_dim, p.neox, a, b);
-            float sn = 0.0f, cs = 1.0f;
-            if (rot) sincosf(posf * fr[j], &sn, &cs);
-            for (uint32_t h = 0; h < G; h++) {
-                float y0 = qs[h * hd + a], y1 = qs[h * hd + b];
-                if (rot) rotate_sc(qs[h * hd + a], qs[h * hd + b], sn, cs, y0, y1);
-                qs[h * hd + a] = y0;
-                qs[h * hd + b] = y1;
+            const bool rot = rope_pair(pp, p.rope_dim, p.neox, a, b) && act;
+            if (!act) a = b = 0;
+            float sn, cs;
+            sincosf(posf * fr[j], &sn, &cs);  // fr = 0 where not rotated
+            float x0[MG], x1[MG];
+#pragma unroll
+            for (int h = 0; h < MG; h++) {
+                x0[h] = qs[h * hd + a];
+                x1[h] = qs[h * hd + b];
             }
-            if (has_new) {
+            if (act) {
+#pragma unroll
+                for (int h = 0; h < MG; h++) {
+                    float y0, y1;
+                    rotate_sc(x0[h], x1[h], sn, cs, y0, y1);
+                    qs[h * hd + a] = rot ? y0 : x0[h];
+                    qs[h * hd + b] = rot ? y1 : x1[h];
+                }
+            }
+            if (has_new && act) {
                 float y0 = ks[a], y1 = ks[b];
                 if (rot) rotate_sc(ks[a], ks[b], sn, cs, y0, y1);
                 const KVT k0 = to_kv<KVT>(y0), k1 = to_kv<KVT>(y1);
@@ -748,19 +761,24 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
                 lrow[w][1][e + 3] = v3;
             }
         }
+        // The operands: 16-byte LDS reads (hd is a multiple of 32 here), unconditional
+        // (other lanes read head 0 and take zeros).
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++) {
             const uint32_t hd0 = 32 * c2 + 8 * g;
             const bool ok = valid && hd0 < hd;
-            const float4 z = float4{0.0f, 0.0f, 0.0f, 0.0f};
-            qb[c2] = q_scaled(ok ? *(const float4*)&qs[n * hd + hd0] : z, ok ? *(const float4*)&qs[n * hd + hd0 + 4] : z, p.sc);
+            const float* src = (const float*)__builtin_assume_aligned(&qs[(valid ? n : 0) * hd + (hd0 < hd ? hd0 : 0)], 16);
+            const f32x4 lo = *(const f32x4*)src, hi = *(const f32x4*)(src + 4);
+            const half8 h = q_scaled(float4{lo[0], lo[1], lo[2], lo[3]}, float4{hi[0], hi[1], hi[2], hi[3]}, p.sc);
+            qb[c2] = ok ? h : half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
         // q stays rotated, as k_rope leaves it. Other units of this KV head may still be
         // reading it, so with several chunks the first one stages the rotated heads and
         // attn_row_fold, which runs after every unit, copies them into q; a lone unit writes q.
         if (c == 0) {
-            float* dst = I.nchunk == 1 ? p.qw + (size_t)I.row * p.nh * hd : p.qrot;
-            for (uint32_t e = lane; e < G * hd; e += 64) dst[(size_t)kvh * G * hd + e] = qs[e];
+            float* dst = (I.nchunk == 1 ? p.qw + (size_t)I.row * p.nh * hd : p.qrot) + (size_t)kvh * G * hd;
+            for (uint32_t e = 4 * lane; e < G * hd; e += 256)
+                *(f32x4*)&dst[e] = *(const f32x4*)__builtin_assume_aligned(&qs[e], 16);
         }
     } else {
 #pragma unroll
