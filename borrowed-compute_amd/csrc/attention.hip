@@ -548,7 +548,6 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
 constexpr int RB = 32;                     // list entries per block of the one-row kernel
 constexpr uint32_t ROW_FUSE_MAXG = 8;      // query heads per KV head a fused step takes
 constexpr uint32_t ROW_MAX_CHUNKS = 256;   // chunks per (item, KV head): attn_row_fold's reach
-constexpr uint32_t ROW_FOLD_BATCH = 16;    // chunk states a thread loads before folding them
 
 template <int HD, typename KVT, bool FUSE>
 __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) {
@@ -925,71 +924,75 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     }
 }
 
-// The fold of a one-row list's chunk states, for one (item, KV head, slot) per workgroup:
-// R thread subsets each fold a contiguous range of chunks from a cleared state, in chunk
-// order (loads of ROW_FOLD_BATCH states issued before the first use), then the R subset
-// states are folded in subset order and normalised. The order is fixed by the chunk count
-// and the shape alone.
+// The fold of a one-row list's chunk states: a workgroup of ROW_FOLD_THREADS per (item, KV
+// head, slot, ROW_FOLD_DIMS dims), so the loads spread over many CUs. R thread subsets of
+// ROW_FOLD_DIMS / 4 threads (four dims each): subset r folds chunks r, r + R, r + 2R, ...
+// in that order from a cleared state (all its loads issued before the first use), then the
+// R subset states merge as a binary tree in LDS (r with r + 1, then r with r + 2, ...) and
+// the root is normalised. The order is fixed by the chunk count and the shape alone.
+constexpr int ROW_FOLD_THREADS = 256;
+constexpr int ROW_FOLD_DIMS = 32;
+
 template <int HD>
-__global__ __launch_bounds__(256) void attn_row_fold(const DirectParams p) {
-    constexpr uint32_t D4 = HD / 4;      // threads per subset: 4 dims each
-    constexpr uint32_t R = 256 / D4;     // subsets
+__global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectParams p) {
+    constexpr uint32_t D4 = ROW_FOLD_DIMS / 4;              // threads per subset: 4 dims each
+    constexpr uint32_t R = ROW_FOLD_THREADS / D4;           // subsets
+    constexpr uint32_t NPT = (ROW_MAX_CHUNKS + R - 1) / R;  // chunks per subset at most
+    constexpr uint32_t NDS = (HD + ROW_FOLD_DIMS - 1) / ROW_FOLD_DIMS;  // dim slices
     __shared__ float4 rO[R][D4];
     __shared__ float2 rML[R][D4];
-    const uint32_t b = blockIdx.x, per_item = p.nkv * p.G;
+    const uint32_t b = blockIdx.x / NDS, ds = blockIdx.x % NDS, per_item = p.nkv * p.G;
     const Item I = p.items[b / per_item];
     const uint32_t nch = I.nchunk;
     if (nch <= 1) return;  // written by the decode kernel
     const uint32_t kvh = (b % per_item) / p.G, s = (b % per_item) % p.G;
-    const uint32_t tid = threadIdx.x, r = tid / D4, d = 4 * (tid % D4);
-    if (p.fuse) {
+    const uint32_t tid = threadIdx.x, r = tid / D4, d = ds * ROW_FOLD_DIMS + 4 * (tid % D4);
+    if (p.fuse && tid < ROW_FOLD_DIMS && ds * ROW_FOLD_DIMS + tid < p.hd) {
         // A fused step: every unit has read q; leave head kvh * G + s rotated.
-        const size_t h = (size_t)kvh * p.G + s;
-        for (uint32_t e = tid; e < p.hd; e += 256) p.qw[((size_t)I.row * p.nh + h) * p.hd + e] = p.qrot[h * p.hd + e];
+        const size_t h = (size_t)kvh * p.G + s, e = ds * ROW_FOLD_DIMS + tid;
+        p.qw[((size_t)I.row * p.nh + h) * p.hd + e] = p.qrot[h * p.hd + e];
     }
-
-    const uint32_t c0 = r * nch / R, c1 = (r + 1) * nch / R;
     const size_t cu0 = (size_t)I.unit0 + (size_t)kvh * nch;
+    float2 ml[NPT];
+    float4 ov[NPT];
+#pragma unroll
+    for (uint32_t q = 0; q < NPT; q++) {
+        const uint32_t c = r + q * R;
+        const size_t at = (cu0 + (c < nch ? c : 0u)) * 16 + s;
+        ml[q] = *(const float2*)(p.part_ml + at * 2);
+        ov[q] = *(const float4*)(p.part_o + at * HD + d);
+    }
     float M = -INFINITY, L = 0.0f;
     float4 O = float4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t cb = c0; cb < c1; cb += ROW_FOLD_BATCH) {
-        float2 ml[ROW_FOLD_BATCH];
-        float4 ov[ROW_FOLD_BATCH];
 #pragma unroll
-        for (uint32_t q = 0; q < ROW_FOLD_BATCH; q++) {
-            const size_t at = (cu0 + min(cb + q, c1 - 1)) * 16 + s;
-            ml[q] = *(const float2*)(p.part_ml + at * 2);
-            ov[q] = *(const float4*)(p.part_o + at * HD + d);
-        }
-#pragma unroll
-        for (uint32_t q = 0; q < ROW_FOLD_BATCH; q++) {
-            if (cb + q < c1) {
-                float a, bb, mn;
-                merge_coef(M, ml[q].x, a, bb, mn);
-                L = L * a + ml[q].y * bb;
-                O = float4{O.x * a + ov[q].x * bb, O.y * a + ov[q].y * bb, O.z * a + ov[q].z * bb, O.w * a + ov[q].w * bb};
-                M = mn;
-            }
+    for (uint32_t q = 0; q < NPT; q++) {
+        if (r + q * R < nch) {
+            float a, bb, mn;
+            merge_coef(M, ml[q].x, a, bb, mn);
+            L = L * a + ml[q].y * bb;
+            O = float4{O.x * a + ov[q].x * bb, O.y * a + ov[q].y * bb, O.z * a + ov[q].z * bb, O.w * a + ov[q].w * bb};
+            M = mn;
         }
     }
     rO[r][tid % D4] = O;
     rML[r][tid % D4] = float2{M, L};
-    __syncthreads();
-    if (r != 0) return;
-    float Mf = -INFINITY, Lf = 0.0f;
-    float4 Of = float4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (uint32_t rr = 0; rr < R; rr++) {
-        const float2 mlr = rML[rr][tid];
-        const float4 orr = rO[rr][tid];
-        float a, bb, mn;
-        merge_coef(Mf, mlr.x, a, bb, mn);
-        Lf = Lf * a + mlr.y * bb;
-        Of = float4{Of.x * a + orr.x * bb, Of.y * a + orr.y * bb, Of.z * a + orr.z * bb, Of.w * a + orr.w * bb};
-        Mf = mn;
+    for (uint32_t step = 1; step < R; step *= 2) {
+        __syncthreads();
+        if (r % (2 * step) == 0) {
+            const float2 o2 = rML[r + step][tid % D4];
+            const float4 oo = rO[r + step][tid % D4];
+            float a, bb, mn;
+            merge_coef(M, o2.x, a, bb, mn);
+            L = L * a + o2.y * bb;
+            O = float4{O.x * a + oo.x * bb, O.y * a + oo.y * bb, O.z * a + oo.z * bb, O.w * a + oo.w * bb};
+            M = mn;
+            rO[r][tid % D4] = O;
+            rML[r][tid % D4] = float2{M, L};
+        }
     }
-    if (d < p.hd)
-        *(float4*)(p.out + ((size_t)I.row * p.nh + kvh * p.G + s) * p.hd + d) = float4{Of.x / Lf, Of.y / Lf, Of.z / Lf, Of.w / Lf};
+    if (r == 0 && d < p.hd)
+        *(float4*)(p.out + ((size_t)I.row * p.nh + kvh * p.G + s) * p.hd + d) = float4{O.x / L, O.y / L, O.z / L, O.w / L};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1608,7 +1611,8 @@ static hipError_t launch_row_t(const DirectParams& dp, bool fold, const AttnCall
         hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, false>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !fold) return e;
-    hipLaunchKernelGGL((attn_row_fold<HD>), dim3(dp.nitems * dp.nkv * dp.G), dim3(256), 0, s, dp);
+    const uint32_t slices = (HD + ROW_FOLD_DIMS - 1) / ROW_FOLD_DIMS;
+    hipLaunchKernelGGL((attn_row_fold<HD>), dim3(dp.nitems * dp.nkv * dp.G * slices), dim3(ROW_FOLD_THREADS), 0, s, dp);
     return hipGetLastError();
 }
 
