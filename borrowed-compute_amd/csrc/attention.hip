@@ -1140,7 +1140,7 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
 // cleared R: the per-element arithmetic of fold(), so a split multi-row call gives the
 // bits of the unsplit one. One thread per (group, slot, 4 dims); each pass issues the
 // loads of CMB_RUN chunk states before the first fold step uses them.
-constexpr int CMB_RUN = 16;
+constexpr int CMB_RUN = 32;  // chunk states a thread loads before folding them (one batch up to 8192 entries)
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_combine(const CombineParams p) {
