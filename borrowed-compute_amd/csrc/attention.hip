@@ -1639,9 +1639,11 @@ static DirectParams direct_params(const AttnCall& a, const Workspace& ws, uint32
 // Chunk of a one-row list with nkv KV heads (each (chunk, KV head) is one wave's unit):
 // a multiple of RB (at least two blocks) that cuts the list into at most ROW_UNITS / nkv
 // chunks, and at most ROW_MAX_CHUNKS. A long step then has about ROW_UNITS waves, four per
-// CU, all issuing their loads from the start (measured at 32768 slots x 8 KV heads: 512
-// units 33.2 us, 1024 units 28.6 us, 2048 units 31.2 us per call). It depends only on the
-// list's own length and nkv, so a sequence gets the same bits in any ragged batch as alone.
+// CU, all issuing their loads from the start. Measured, decode kernel at 32768 slots x 8 KV
+// heads: ROW_UNITS 768: 26.9 us, 896: 26.5, 1024 (912 units of 288 entries): 24.9, 1536:
+// 30.2, 2048: 26.4; 1024 units of 257 entries (not a multiple of RB; 256 workgroups): 28.0.
+// It depends only on the list's own length and nkv, so a sequence gets the same bits in any
+// ragged batch as alone.
 constexpr uint64_t ROW_UNITS = 1024;
 
 uint32_t row_chunk(uint64_t len, uint32_t nkv) {
