@@ -91,6 +91,13 @@ DECODE = [
     (8, 8, 256, 300, bchip.F16),
     (16, 1, 128, 200, bchip.F16),   # a group of 16
     (12, 3, 40, 150, bchip.F32),    # head_dim padded inside the kernel
+    # The one-row kernel takes a list's last entry as a block of its own after the last
+    # chunk's stream: lists whose last chunk holds that entry alone (chunks of 64 entries).
+    (32, 8, 128, 257, bchip.F16),
+    (32, 8, 128, 4097, bchip.F16),
+    (28, 4, 128, 8193, bchip.F16),
+    (14, 2, 64, 129, bchip.F32),
+    (32, 8, 128, 32769, bchip.F16),  # configs[1]'s step: 114 chunks of 288, the last of 225
 ]
 
 
