@@ -564,7 +564,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     // 25.9 against 28.0 us at 32768 slots x 8 KV heads, and 131 against 154 us for the
     // ragged batch).
     constexpr bool KL = sizeof(KVT) == 2 && HD <= 128;
-    constexpr int KS = HD + 8;  // LDS row stride of K (halves): rows 4 banks apart
+    constexpr int KS = HD + 8;  // LDS row stride of K (halves): rows 4 banks apart (4 or 16, 24: slower)
     __shared__ __attribute__((aligned(16))) f16 kt[KL ? 4 : 1][KL ? RB * KS : 8];
     // The list's last entry (a fused step's new row) as the cache holds it, per wave: K then
     // V, dims past hd zero. The chunk that holds it takes it as a block of its own, after
