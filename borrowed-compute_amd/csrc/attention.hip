@@ -564,7 +564,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     // 25.9 against 28.0 us at 32768 slots x 8 KV heads, and 131 against 154 us for the
     // ragged batch).
     constexpr bool KL = sizeof(KVT) == 2 && HD <= 128;
-    constexpr int KS = HD + 8;  // LDS row stride of K (halves): rows 4 banks apart (4 or 16, 24: slower)
+    constexpr int KS = HD + 8;  // LDS row stride of K (halves): rows 4 banks apart (pads of 4, 16, 24 measured slower)
     __shared__ __attribute__((aligned(16))) f16 kt[KL ? 4 : 1][KL ? RB * KS : 8];
     // The list's last entry (a fused step's new row) as the cache holds it, per wave: K then
     // V, dims past hd zero. The chunk that holds it takes it as a block of its own, after
@@ -585,9 +585,9 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = rem % p.nkv;
     const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, I.len);
     // The last chunk streams up to the list's last entry and then takes that entry alone:
-    // the same blocks whether the entry came from the cache or, in a fused step, from
-    // registers (so both give the same bits), and no block of the stream holds a slot this
-    // kernel writes.
+    // the same blocks whether the entry came from the cache or, in a fused step, from this
+    // kernel's own rotation (so both give the same bits), and no block of the stream holds a
+    // slot this kernel writes.
     const uint32_t last = I.len - 1;
     const bool has_last = kb1 == I.len;
     const uint32_t kbs = has_last ? last : kb1;  // end of the streamed entries
@@ -596,8 +596,8 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
     const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
 
-    // Block key0 into registers; entries at or past kbs read the zero page (no HBM traffic,
-    // no branch between the loads).
+    // Block key0's K or V into registers; entries at or past kbs read the zero page (no HBM
+    // traffic, no branch between the loads).
     auto load_k = [&](uint32_t key0, Raw<KVT> (&kr)[2][NKC]) {
         if constexpr (KL) {
             // Row-contiguous: load i holds entry key0 + i VRI + lane / VLR, dims 8 (lane % VLR).
