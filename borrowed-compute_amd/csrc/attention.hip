@@ -175,7 +175,7 @@ template <int HD, int NT, typename KOp, typename VOp>
 __device__ __forceinline__ void block_step(State<HD / 16> (&s)[NT], const half8 (&qb)[NT][HD / 32], KOp kop,
                                            VOp vop, uint32_t key0, const uint32_t (&len)[NT]) {
     const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, n = lane & 15;
+    const int g = lane >> 4;
     f32x4 st[NT][4];
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
@@ -328,8 +328,8 @@ __device__ __forceinline__ void store_state(const State<NDT>& st, float* o_row, 
     if (write_ml) *(float2*)ml = float2{st.m, st.l};
 }
 
-template <int HD, typename KVT, bool TREE>
-__global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(const DirectParams p) {
+template <int HD, typename KVT>
+__global__ __launch_bounds__(256, sizeof(KVT) == 2 && HD <= 128 ? 4 : 2) void attn_decode(const DirectParams p) {
     constexpr int NDT = HD / 16;                     // output tiles of 16 dims
     constexpr int DTW = NDT >= 4 ? NDT / 4 : 1;      // output tiles per wave
     constexpr int DW = 16 * DTW;                     // dims per wave
@@ -350,9 +350,8 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     const uint32_t hd = p.hd, kvd = p.nkv * hd;
     const KVT* zp = (const KVT*)p.zero;
 
-    // One unit per workgroup (multi-row lists: tree rows and short lines), in (item, chunk,
-    // KV head) order: the KV heads of one chunk
-    // read one stretch of the cache together. Consecutive workgroups go to the 8 XCDs in
+    // One unit per workgroup (tree rows), in (item, chunk, KV head) order: the KV heads of
+    // one chunk read one stretch of the cache together. Consecutive workgroups go to the 8 XCDs in
     // turn, so the KV head turns with the chunk (j + c) to give every XCD a mix of heads:
     // a fixed head per XCD leaves the XCDs whose head's cache columns map to busier HBM
     // channels finishing last. The state is stored at the unit's canonical index.
@@ -362,30 +361,25 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 ? 4 : 2) void attn_decode(con
     const Item I = p.items[it];
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = (rem % p.nkv + c) % p.nkv;
     const size_t cu = (size_t)I.unit0 + (size_t)c * p.nkv + kvh;
-    // Slot n of an item is row I.row + n / G, head kvh * G + n % G (an item holds nrows
-    // consecutive rows of a line, or one tree row); row I.row + j sees I.len + j list
-    // entries.
+    // Slot n of an item is row I.row + n / G, head kvh * G + n % G (an item is one tree
+    // row: nrows = 1).
     const uint32_t srow = n / p.G, shead = kvh * p.G + n % p.G;
     const bool valid = srow < I.nrows;
     const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
     const KVT* vc = (const KVT*)p.vc + I.kvoff * kvd + (size_t)kvh * hd;
-    uint32_t len = I.len + I.nrows - 1;  // the longest list among the item's rows
-    if constexpr (TREE) {
-        const uint32_t lo = p.masks[2 * I.row], hi = p.masks[2 * I.row + 1];
-        const uint32_t ntail = __popc(lo) + __popc(hi);
-        len = p.base + ntail;
-        if ((uint32_t)tid < ntail) tail[tid] = p.base + nth_set_bit(lo, hi, tid);
-        __syncthreads();
-    }
-    const uint32_t lane_len = TREE ? len : I.len + (valid ? srow : 0u);  // this slot's list
+    // The row's list: the slots below base, then base + j for each set bit j of its mask.
+    const uint32_t lo = p.masks[2 * I.row], hi = p.masks[2 * I.row + 1];
+    const uint32_t ntail = __popc(lo) + __popc(hi);
+    const uint32_t len = p.base + ntail;
+    if ((uint32_t)tid < ntail) tail[tid] = p.base + nth_set_bit(lo, hi, tid);
+    __syncthreads();
+    const uint32_t lane_len = len;  // this slot's list
     const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, len);
 
     // Cache slot of list entry k, or ok = false for entries past the list (and for tree
-    // slots past the cache, which a bad mask could name): those read as zeros. A line's
-    // slot is its list entry, with no branch between the loads of a block.
+    // slots past the cache, which a bad mask could name): those read as zeros.
     auto slot_of = [&](uint32_t k, bool& ok) -> uint32_t {
         ok = k < len;
-        if constexpr (!TREE) return ok ? k : 0u;
         if (!ok) return 0u;
         const uint32_t s = k < p.base ? k : tail[k - p.base];
         ok = (uint64_t)s + I.kvoff < p.slot_limit;
@@ -1592,11 +1586,9 @@ static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream
 
 template <int HD, typename KVT>
 static hipError_t launch_decode_t(DirectParams& dp, CombineParams& cp, const AttnCall& a, hipStream_t s) {
-    const dim3 block(256);
-    if (dp.tree)
-        hipExtLaunchKernelGGL((attn_decode<HD, KVT, true>), dim3(dp.nunits), block, 0, s, a.ev_before, a.ev_after, 0, dp);
-    else
-        hipExtLaunchKernelGGL((attn_decode<HD, KVT, false>), dim3(dp.nunits), block, 0, s, a.ev_before, a.ev_after, 0, dp);
+    // Tree rows only: lines of any length go to the shared kernels, one-row lists to the
+    // one-row kernel.
+    hipExtLaunchKernelGGL((attn_decode<HD, KVT>), dim3(dp.nunits), dim3(256), 0, s, a.ev_before, a.ev_after, 0, dp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_combine_t<HD>(cp, dp.nitems * dp.nkv, s);

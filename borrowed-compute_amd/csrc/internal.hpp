@@ -57,7 +57,7 @@ struct RopeArgs {
 };
 hipError_t row_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s);
 bool row_fusable(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox);
-// Multi-row items (tree rows, short lines) with chunk and nchunk set.
+// Tree rows as items with chunk and nchunk set (CHUNK_MULTI).
 hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
                             Workspace& ws, hipStream_t s);
 hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s);
