@@ -201,7 +201,9 @@ int bchip_init(int device, bchip_ctx** out) {
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
     bchip_ctx* c = new bchip_ctx();
     c->device = device;
-    c->name = prop.name;
+    // The marketing name can be empty (some runtimes leave it blank): fall back to the ISA.
+    c->name = std::string(prop.name[0] ? prop.name : prop.gcnArchName) + " (" +
+              std::to_string(prop.multiProcessorCount) + " CUs)";
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = c->ws.init();
     if (e == hipSuccess) e = hipEventCreate(&c->t0);
