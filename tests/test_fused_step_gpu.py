@@ -40,6 +40,8 @@ CASES = [
     (8, 8, 256, 256, False, 1e4, bchip.F16, 700),      # head_dim 256
     (32, 8, 128, 96, True, 5e5, bchip.F16, 100),       # neox pairs 48 apart: the two-call path
     (4, 2, 16, 16, False, 1e4, bchip.F32, 6),          # tiny_model shape (hd 16): the two-call path
+    (16, 1, 128, 128, False, 5e5, bchip.F16, 200),     # 16 query heads per KV head: the two-call path
+    (16, 2, 128, 128, False, 5e5, bchip.F16, 256),     # 8 per KV head, the last chunk holds the new row alone
 ]
 
 
