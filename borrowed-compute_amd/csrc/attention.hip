@@ -679,13 +679,15 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
             qc[c2] = *(const float4*)(src + 4);
         }
     }
-    Raw<KVT> kR[2][2][NKC], vR[NVL];
+    Raw<KVT> kR[2][2][NKC], vR[NVL], vR2[NVL];
+    // A stream of at most two blocks (short lists) has all of it in flight through the
+    // prologue; a longer one has the first block and the second block's K.
+    const bool two = kbs <= kb0 + 2 * RB;
     if constexpr (DB) {
-        // The first block, and the second block's K: in flight through the prologue (the
-        // wait for q, the rotation of a fused step).
         load_k(kb0, kR[0]);
         load_v(kb0, vR);
         load_k(kb0 + RB, kR[1]);
+        if (two) load_v(kb0 + RB, vR2);
     }
     if constexpr (FUSE) {
         // q, k and v into the LDS tile; then each lane rotates its pairs there (the angle
@@ -861,8 +863,13 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         // flight there. A chunk with an even block count computes one block past its end: its
         // entries are all masked (P = 0 exactly, the max and the scale hold), its loads read
         // the zero page, and the state comes out unchanged.
-        compute_block(kb0, kbs, kR[0], vR, [&] { load_v(kb0 + RB, vR); });
-        for (uint32_t key0 = kb0 + RB; key0 < kbs; key0 += 2 * RB) {
+        if (two) {
+            compute_block(kb0, kbs, kR[0], vR, nothing);
+            if (kb0 + RB < kbs) compute_block(kb0 + RB, kbs, kR[1], vR2, nothing);
+        } else {
+            compute_block(kb0, kbs, kR[0], vR, [&] { load_v(kb0 + RB, vR); });
+        }
+        for (uint32_t key0 = two ? kbs : kb0 + RB; key0 < kbs; key0 += 2 * RB) {
 #pragma unroll
             for (int s = 0; s < 2; s++) {
                 const uint32_t kb = key0 + s * RB;
