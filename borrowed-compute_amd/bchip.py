@@ -19,7 +19,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "bchip.h")
 
 F32, F16 = 0, 1
 OK, E_ARG, E_HIP, E_NODEV, E_DISABLED, E_UNSUPPORTED, E_OOM = 0, -1, -2, -3, -4, -5, -6
-CHUNK_MULTI = 256
+CHUNK_MULTI = 192
 
 _lib = None
 

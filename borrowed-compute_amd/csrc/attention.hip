@@ -1199,7 +1199,7 @@ __global__ __launch_bounds__(256) void attn_combine(const CombineParams p) {
 
 // ---------------------------------------------------------------------------------------
 // Prefill kernel (f16 caches, hd 128): the shared kernel's slots and arithmetic (block_step
-// per 64-entry block, chunk states folded every 256 entries), with K and V blocks copied
+// per 64-entry block, chunk states folded every 192 entries), with K and V blocks copied
 // HBM -> LDS by the gfx950 direct-to-LDS loads, so that no VGPR holds a block in flight.
 // Each load instruction of a wave fills 1 KB of LDS in lane order: four whole cache rows,
 // lane l taking row 4q + l/16 and 16-byte chunk (l % 16) ^ f(row) of it, so the LDS rows
@@ -1256,44 +1256,45 @@ __global__ __launch_bounds__(256) void vt_pack(const f16* __restrict__ vc, f16* 
 }
 
 // The prefill kernel proper: one 16-slot tile per wave, W waves sharing each K and V block
-// in LDS, block_step's arithmetic. Blocks stream through a ring of STAGES LDS stages (one
-// LDS object each, K then V), fetched STAGES-1 blocks ahead by direct-to-LDS loads, with one
-// barrier per block (measured: a 4-stage ring 465 / 613 TFLOP/s at 2048 / 8192 rows against
-// 411 / 574 with 2 stages). The loop is unrolled by STAGES so that every stage is a
-// compile-time object: the compiler then waits for a stage's own loads before reading it,
-// not for every load in flight. (Computing block b+1's scores beside block b's softmax
-// needs both blocks' scores live at once: past the 256 registers of two waves per SIMD,
-// and the spill reloads then wait for the whole ring: 246 / 308 TFLOP/s.)
-// The per-block work is cut to what the arithmetic needs (the loop is VALU-bound before it
-// is MFMA- or LDS-bound: 8.7 VALU instructions per MFMA in a straightforward build, where
-// about two per MFMA issue alongside the MFMAs for free):
+// in LDS, block_step's arithmetic per slot. Blocks stream through a ring of three LDS
+// stages (one LDS object each, K then V), one chunk's worth, fetched two blocks ahead by
+// direct-to-LDS loads, with one barrier per block. The loop is unrolled by the chunk, so
+// that every stage is a compile-time object (the compiler then waits for a stage's own
+// loads before reading it, not for every load in flight) and the chunk fold sits in
+// straight-line code between chunks (measured against a four-stage ring with the fold
+// behind a branch: 505 / 640 TFLOP/s at 2048 / 8192 rows against 491 / 625, and verify
+// 11.9 µs against 14.0 at 4096 slots).
+// Not kept (measured slower): two tiles a wave at one wave a SIMD (each V operand read
+// once for two MFMAs, one tile's softmax scheduled beside the other's MFMAs, R in LDS):
+// 370 / 460 TFLOP/s; raising a wave's priority over its MFMAs: 3-7% slower.
+// The per-block work is cut to what the arithmetic needs:
 //  - rows are fetched from per-lane offsets fixed for the whole loop plus a scalar block
 //    base; only a block that ends past the list selects the zero page per lane, and nothing
 //    past the list is fetched;
-//  - LDS operand reads are per-lane bases plus immediate offsets;
+//  - the mask test is one vote per tile; LDS operand reads are per-lane bases plus
+//    immediate offsets;
 //  - P is rounded to f16 once, for both the block sum and the PV operand.
 template <int N>
 using ic = std::integral_constant<int, N>;
 
-template <int W, bool VT, int STAGES>
+template <int W, bool VT>
 __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     constexpr int HD = 128;
     constexpr int NKC = HD / 32, NDT = HD / 16;
+    constexpr int STAGES = CHUNK_MULTI / BLK;   // ring stages: one chunk
     constexpr int RPI = 64 / PF_CPR;            // cache rows per load instruction
     constexpr int LPW = BLK / RPI / W;          // load instructions per wave per block (K or V)
     constexpr int LPB = 2 * LPW;                // K and V loads per wave per block
     constexpr int SZ = 2 * BLK * HD;            // f16 per stage: K rows, then V (or V^T)
     static_assert(LPW * RPI * W == BLK, "a block's rows divide over the waves");
-    static_assert(STAGES == 3 || STAGES == 4, "ring of 3 or 4 stages");
+    static_assert(STAGES == 3 && CHUNK_MULTI % BLK == 0, "the loop below is unrolled by three blocks");
     __shared__ __attribute__((aligned(16))) f16 ring0[SZ];
     __shared__ __attribute__((aligned(16))) f16 ring1[SZ];
     __shared__ __attribute__((aligned(16))) f16 ring2[SZ];
-    __shared__ __attribute__((aligned(16))) f16 ring3[STAGES > 3 ? SZ : 8];
     auto ring = [&](auto S) -> f16* {
         if constexpr (decltype(S)::value == 0) return ring0;
         else if constexpr (decltype(S)::value == 1) return ring1;
-        else if constexpr (decltype(S)::value == 2) return ring2;
-        else return ring3;
+        else return ring2;
     };
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1394,16 +1395,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     for (int c = 0; c < NKC; c++) kbase[c] = n * HD + 8 * ((4 * c + g) ^ n);
 #pragma unroll
     for (int kc = 0; kc < 2; kc++) vbase[kc] = n * BLK + 8 * ((4 * kc + g) ^ (n % 8));
-    // S^T = K . Q^T of the block in stage S: four key tiles, hd chunks accumulated in order.
-    auto scores = [&](auto S, f32x4 (&sc4)[4]) {
-        const f16* kls = ring(S);
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            sc4[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int c = 0; c < NKC; c++) sc4[kt] = mfma16(*(const half8*)&kls[kbase[c] + kt * 16 * HD], qb[c], sc4[kt]);
-        }
-    };
     // Barrier without the fence __syncthreads carries: that fence would wait for every
     // direct-to-LDS load in flight, the later blocks' included. The waits before it are
     // explicit; LDS reads of a wave finish before its MFMAs consume them, so every read of a
@@ -1417,68 +1408,27 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     State<NDT> R, cs;
     state_clear(R);
     state_clear(cs);
-    // Prologue: blocks 0 .. STAGES-2 in flight, block 0 in, its scores. (A workgroup of a
-    // split launch may see nothing of its chunk: then it only stores its empty state.)
-    f32x4 scur[4];
+    // Prologue: blocks 0 .. STAGES-2 in flight. (A workgroup of a split launch may see
+    // nothing of its chunk: then it only stores its empty states.)
     if (kb0 < kb1) {
         load_block(kb0, ic<0>{});
         load_block(kb0 + BLK, ic<1>{});
-        if constexpr (STAGES > 3) load_block(kb0 + 2 * BLK, ic<2>{});
     }
 #pragma unroll
     for (int c = 0; c < NKC; c++) qb[c] = q_scaled(qraw[c][0], qraw[c][1], p.sc);
-    if (kb0 < kb1) {
-        // wait for block 0 alone: every later prologue block that was issued may still load
-        if (STAGES > 3 && kb0 + 2 * BLK < kb1)
-            wait_vm<2 * LPB>();
-        else if (kb0 + BLK < kb1)
-            wait_vm<LPB>();
-        else
-            wait_vm<0>();
-        barrier();
-    }
 
-    // One block: S = stage of block b (its V; its K was read one block earlier).
-    auto iter = [&](uint32_t key0, auto S) -> bool {
-        constexpr int s0 = decltype(S)::value;
-        constexpr int sr = (s0 + STAGES - 1) % STAGES;
-        const uint32_t key1 = key0 + BLK;
-        // Block b+1 in (own loads: wait, leaving block b+2's in flight; everyone's: the
-        // barrier), and every read of the stage that block b+STAGES-1 refills is over.
-        if (key1 < kb1) {
-            if (STAGES > 3 && key1 + BLK < kb1)
-                wait_vm<LPB * (STAGES - 3)>();
-            else
-                wait_vm<0>();
-        }
-        barrier();
-        load_block(key0 + (STAGES - 1) * BLK, ic<sr>{});
-        if (key0 != kb0 && key0 % CHUNK_MULTI == 0) {
-            keep_branch();
-            fold(R, cs);
-            state_clear(cs);
-        }
-        scores(S, scur);
-        float x[4][4];
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) x[kt][i] = scur[kt][i];
-        if (!__all(key0 + BLK <= len)) {
-            keep_branch();
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (key0 + 16 * kt + 4 * g + i >= len) x[kt][i] = -INFINITY;
-        }
+    // The softmax of the tile over a block (block_step's): scores in log2 units -> the P^T
+    // operands pb (f16) and the tile's new max and sum; corr is the factor its O takes
+    // before the block's PV.
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    auto softmax = [&](State<NDT>& s, const f32x4 (&x)[4], half8 (&pb)[2], float& corr) {
         float mx = fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3]));
 #pragma unroll
         for (int kt = 1; kt < 4; kt++)
             mx = fmaxf(mx, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
         mx = tile_max(mx);
-        float mn, ms, corr;
-        lazy_max(cs.m, mx, mn, ms, corr);
+        float mn, ms;
+        lazy_max(s.m, mx, mn, ms, corr);
         // P in f16 once: the block sum (dot2 chain over the pairs, tiles in order, then across
         // lanes) and the PV operand (keys 32kc + 4g + 0..3, then 32kc + 16 + 4g + 0..3).
         uint32_t hp[4][2];
@@ -1492,15 +1442,52 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
                 hp[kt][j] = __builtin_bit_cast(uint32_t, h);
             }
         const float ps = tile_sum(ls);
-        cs.l = cs.l * corr + ps;
-        cs.m = mn;
-        rescale(cs.o, corr);
-        // PV of block b.
-        const f16* vls = ring(S) + BLK * HD;
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        s.l = s.l * corr + ps;
+        s.m = mn;
 #pragma unroll
-        for (int kc = 0; kc < 2; kc++) {
-            const half8 pb = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
+        for (int kc = 0; kc < 2; kc++)
+            pb[kc] = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
+    };
+    // One block in stage S: scores, mask, softmax, PV.
+    auto iter = [&](uint32_t key0, auto S) -> bool {
+        constexpr int s0 = decltype(S)::value;
+        const uint32_t key1 = key0 + BLK;
+        // This block in (own loads: wait, leaving the next block's in flight; everyone's:
+        // the barrier), and every read of the stage that block b+2 refills (block b-1's) is
+        // over.
+        if (key1 < kb1)
+            wait_vm<LPB>();
+        else
+            wait_vm<0>();
+        barrier();
+        load_block(key0 + (STAGES - 1) * BLK, ic<(s0 + STAGES - 1) % STAGES>{});
+        // S^T = K . Q^T: four key tiles, hd chunks accumulated in order.
+        const f16* kls = ring(S);
+        f32x4 sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            sc[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < NKC; c++) sc[kt] = mfma16(*(const half8*)&kls[kbase[c] + kt * 16 * HD], qb[c], sc[kt]);
+        }
+        // Entries at or past a slot's list length are masked (a block every slot of the
+        // tile sees whole skips the test).
+        if (!__all(key0 + BLK <= len)) {
+            keep_branch();
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (key0 + 16 * kt + 4 * g + i >= len) sc[kt][i] = -INFINITY;
+        }
+        half8 pb[2];
+        float corr;
+        softmax(cs, sc, pb, corr);
+        rescale(cs.o, corr);
+        // PV of the block.
+        const f16* vls = ring(S) + BLK * HD;
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++)
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
                 half8 a;
@@ -1515,21 +1502,19 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
                     const half4 hi = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
                     a = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 }
-                cs.o[dt] = mfma16(a, pb, cs.o[dt]);
+                cs.o[dt] = mfma16(a, pb[kc], cs.o[dt]);
             }
-        }
         return key1 < kb1;
     };
-    for (uint32_t key0 = kb0; key0 < kb1;) {
-        if (!iter(key0, ic<0>{})) break;
-        key0 += BLK;
-        if (!iter(key0, ic<1>{})) break;
-        key0 += BLK;
-        if (!iter(key0, ic<2>{})) break;
-        key0 += BLK;
-        if constexpr (STAGES > 3) {
-            if (!iter(key0, ic<3 % STAGES>{})) break;
-            key0 += BLK;
+    // Chunk by chunk: three blocks, then (when the list goes on) the chunk's fold into R and
+    // a fresh state.
+    if (kb0 < kb1) {
+        for (uint32_t key0 = kb0;; key0 += CHUNK_MULTI) {
+            if (!iter(key0, ic<0>{})) break;
+            if (!iter(key0 + BLK, ic<1>{})) break;
+            if (!iter(key0 + 2 * BLK, ic<2>{})) break;
+            fold(R, cs);
+            state_clear(cs);
         }
     }
     if (p.split) {
@@ -1810,11 +1795,11 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
                                (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, sp.vt_npad);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
-            hipExtLaunchKernelGGL((attn_prefill<8, true, 4>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
+            hipExtLaunchKernelGGL((attn_prefill<8, true>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else if (wide) {
-            hipExtLaunchKernelGGL((attn_prefill<8, false, 4>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
+            hipExtLaunchKernelGGL((attn_prefill<8, false>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else {
-            hipExtLaunchKernelGGL((attn_prefill<4, false, 4>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
+            hipExtLaunchKernelGGL((attn_prefill<4, false>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
         }
         e = hipGetLastError();
     } else {

@@ -20,7 +20,7 @@ constexpr int BLK = 64;
 // a fresh state, so a chunk may be computed by any workgroup and the row's bits do not
 // change: that is what lets a speculative verify split across CUs and still match a
 // prefill row exactly.
-constexpr uint32_t CHUNK_MULTI = 256;
+constexpr uint32_t CHUNK_MULTI = 192;
 // Largest head dimension (the reference's MAX_HEAD, kernels.h:31).
 constexpr uint32_t MAX_HD = 256;
 // Rows a tree pass may hold (model.rs:408), and items one direct launch takes.
