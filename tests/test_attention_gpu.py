@@ -145,6 +145,8 @@ PREFILL = [
     (8, 1000, 16, 1, 128, bchip.F16),
     (5, 600, 14, 2, 64, bchip.F32),     # short line, G = 7: units of 2 rows, f32 cache
     (3, 2000, 28, 4, 128, bchip.F16),   # short line over 8 chunks, G = 7
+    (2, 190, 32, 8, 128, bchip.F16),    # lists of 191 and 192: the second ends a chunk
+    (4, 381, 28, 4, 128, bchip.F16),    # lists 382..385 across the second chunk's end
 ]
 
 
@@ -198,7 +200,9 @@ def test_batch_invariance_and_determinism(ctx):
 
 def test_split_and_unsplit_give_the_same_bits(ctx):
     """8 verify rows at a long context split across CUs by chunk; the same rows inside a
-    large batch are folded in one workgroup: identical bits (the chunk fold is fixed)."""
+    large batch are folded in one workgroup: identical bits (the chunk fold is fixed). And
+    every row of the large batch against passes of 200 rows, which take the other prefill
+    kernel (V read by transposing LDS reads, split by chunk)."""
     nh, nkv, hd = 32, 8, 128
     pos = 3000
     big = 2100  # 8 kv heads x 66 row blocks of 32: enough workgroups to run unsplit
@@ -210,6 +214,12 @@ def test_split_and_unsplit_give_the_same_bits(ctx):
     for r0 in (0, 1000, 2092):
         part = a.run(q[r0:r0 + 8], 8, pos + r0, 0.0884)
         np.testing.assert_array_equal(part, whole[r0:r0 + 8], err_msg=f"rows {r0}..")
+    # Every row of the big pass (the packed-V^T kernel) against passes of 200 rows (too few
+    # workgroups to run unsplit: the transposing-read kernel, split by chunk, combined).
+    for r0 in range(0, big, 200):
+        n = min(200, big - r0)
+        part = a.run(q[r0:r0 + n], n, pos + r0, 0.0884)
+        np.testing.assert_array_equal(part, whole[r0:r0 + n], err_msg=f"rows {r0}.. in a pass of {n}")
     a.free()
 
 
