@@ -68,6 +68,11 @@ def lib() -> ctypes.CDLL:
         "bchip_rope_append_attention": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32, P], i32),
         "bchip_attention_ragged": ([P, P, P, P, u32, P, P, P, u32, u32, u32, u32, f32], i32),
         "bchip_fill_normal": ([P, P, u32, u64, u64], i32),
+        "bchip_matmul": ([P, P, u32, P, P, u32, u32, u32], i32),
+        "bchip_rms_norm": ([P, P, P, P, u32, u32, f32], i32),
+        "bchip_bias_add": ([P, P, P, u64, u32], i32),
+        "bchip_silu_mul": ([P, P, P, u64], i32),
+        "bchip_add": ([P, P, P, u64], i32),
         "bchip_timer_start": ([P], i32),
         "bchip_timer_stop": ([P, P], i32),
         "bchip_timer_arm": ([P, P, P], i32),
@@ -210,6 +215,21 @@ class Ctx:
         check(lib().bchip_attention_ragged(self.h, _ptr(q), _ptr(kc), _ptr(vc), kv_type, _ptr(out),
                                            lens.ctypes.data_as(ctypes.c_void_p),
                                            offs.ctypes.data_as(ctypes.c_void_p), len(lens), nh, nkv, hd, scale))
+
+    def matmul(self, w, wtype, x, out, rows, cols, n) -> None:
+        check(lib().bchip_matmul(self.h, _ptr(w), wtype, _ptr(x), _ptr(out), rows, cols, n))
+
+    def rms_norm(self, x, w, out, rows, cols, eps) -> None:
+        check(lib().bchip_rms_norm(self.h, _ptr(x), _ptr(w), _ptr(out), rows, cols, eps))
+
+    def bias_add(self, x, b, n, dim) -> None:
+        check(lib().bchip_bias_add(self.h, _ptr(x), _ptr(b), n, dim))
+
+    def silu_mul(self, g, u, n) -> None:
+        check(lib().bchip_silu_mul(self.h, _ptr(g), _ptr(u), n))
+
+    def add(self, x, y, n) -> None:
+        check(lib().bchip_add(self.h, _ptr(x), _ptr(y), n))
 
     def fill_normal(self, dst, t, n, seed) -> None:
         check(lib().bchip_fill_normal(self.h, _ptr(dst), t, n, seed))

@@ -328,6 +328,61 @@ int bchip_rope(bchip_ctx* c, float* x, const float* inv_freq, const uint32_t* po
     return BCHIP_OK;
 }
 
+int bchip_matmul(bchip_ctx* c, const void* w, uint32_t type, const float* x, float* out, uint32_t rows,
+                 uint32_t cols, uint32_t n) {
+    CHECK(enter(c));
+    if (rows == 0 || n == 0) return BCHIP_OK;
+    if (!w || !x || !out) return fail(BCHIP_E_ARG, "null pointer");
+    uint32_t bw, bb;
+    if (!ggml_block(type, bw, bb)) return fail(BCHIP_E_UNSUPPORTED, "ggml type %u", type);
+    if (cols == 0 || cols % 32 || cols % bw) return fail(BCHIP_E_ARG, "cols %u: not whole groups of 32 and blocks of %u", cols, bw);
+    if ((uintptr_t)w % 16 || (uintptr_t)x % 16) return fail(BCHIP_E_ARG, "w and x must be 16-byte aligned");
+    const uint64_t row_bytes = (uint64_t)cols / bw * bb;
+    CHECK(check_span(c, w, row_bytes * rows, "weights"));
+    CHECK(check_span(c, x, (uint64_t)n * cols * 4, "x"));
+    CHECK(check_span(c, out, (uint64_t)n * rows * 4, "out"));
+    HIP_TRY(matmul_launch(w, type, x, out, rows, cols, n, (uint32_t)row_bytes, c->stream), "matmul");
+    return BCHIP_OK;
+}
+
+int bchip_rms_norm(bchip_ctx* c, const float* x, const float* w, float* out, uint32_t rows, uint32_t cols, float eps) {
+    CHECK(enter(c));
+    if (rows == 0) return BCHIP_OK;
+    if (!x || !w || !out) return fail(BCHIP_E_ARG, "null pointer");
+    if (cols == 0) return fail(BCHIP_E_ARG, "cols 0");
+    CHECK(check_span(c, x, (uint64_t)rows * cols * 4, "x"));
+    CHECK(check_span(c, w, (uint64_t)cols * 4, "w"));
+    CHECK(check_span(c, out, (uint64_t)rows * cols * 4, "out"));
+    const bool vec = cols % 4 == 0 && ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) % 16 == 0;
+    HIP_TRY(rms_norm_launch(x, w, out, rows, cols, eps, vec, c->stream), "rms_norm");
+    return BCHIP_OK;
+}
+
+static int elementwise(bchip_ctx* c, int op, float* x, const float* y, uint64_t n, uint32_t dim, uint64_t y_len,
+                       const char* what) {
+    CHECK(enter(c));
+    if (n == 0) return BCHIP_OK;
+    if (!x || !y) return fail(BCHIP_E_ARG, "null pointer");
+    CHECK(check_span(c, x, n * 4, what));
+    CHECK(check_span(c, y, y_len * 4, what));
+    HIP_TRY(elementwise_launch(op, x, y, n, dim, c->stream), what);
+    return BCHIP_OK;
+}
+
+int bchip_bias_add(bchip_ctx* c, float* x, const float* b, uint64_t n, uint32_t dim) {
+    if (dim == 0) {
+        CHECK(enter(c));
+        return fail(BCHIP_E_ARG, "bias of dim 0");
+    }
+    return elementwise(c, EW_BIAS, x, b, n, dim, dim, "bias_add");
+}
+
+int bchip_silu_mul(bchip_ctx* c, float* g, const float* u, uint64_t n) {
+    return elementwise(c, EW_SILU_MUL, g, u, n, 1, n, "silu_mul");
+}
+
+int bchip_add(bchip_ctx* c, float* x, const float* y, uint64_t n) { return elementwise(c, EW_ADD, x, y, n, 1, n, "add"); }
+
 int bchip_copy(bchip_ctx* c, const void* src, uint32_t st, void* dst, uint32_t dt, uint64_t off, uint64_t n) {
     CHECK(enter(c));
     if (n == 0) return BCHIP_OK;

@@ -74,4 +74,13 @@ hipError_t keep_launch(void* const* bufs, uint32_t nbufs, uint32_t type, uint32_
                        const uint32_t* rows, uint32_t nrows, hipStream_t s);
 hipError_t fill_normal_launch(void* dst, uint32_t type, uint64_t n, uint64_t seed, hipStream_t s);
 
+// The rest of a layer (layer.hip).
+bool ggml_block(uint32_t type, uint32_t& weights, uint32_t& bytes);
+hipError_t matmul_launch(const void* w, uint32_t type, const float* x, float* out, uint32_t rows, uint32_t cols,
+                         uint32_t n, uint32_t row_bytes, hipStream_t s);
+hipError_t rms_norm_launch(const float* x, const float* w, float* out, uint32_t rows, uint32_t cols, float eps,
+                           bool vec, hipStream_t s);
+enum : int { EW_BIAS = 0, EW_SILU_MUL = 1, EW_ADD = 2 };
+hipError_t elementwise_launch(int op, float* x, const float* y, uint64_t n, uint32_t dim, hipStream_t s);
+
 }  // namespace bchip

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BCHIP_ABI_VERSION 1
+#define BCHIP_ABI_VERSION 2
 
 enum bchip_type { BCHIP_F32 = 0, BCHIP_F16 = 1 }; /* T_F32 / T_F16 of kernels.h:14-15 */
 
@@ -154,6 +154,46 @@ int bchip_attention_ragged(bchip_ctx* ctx, const float* q, const void* kc, const
                            uint32_t kv_type, float* out, const uint32_t* seq_lens,
                            const uint64_t* kv_offsets, uint32_t nseq, uint32_t nh,
                            uint32_t nkv, uint32_t hd, float scale);
+
+/* ---- The rest of a layer (Layers::forward, mod.rs:454-491): the GGUF block-format
+ * product, RMSNorm and the elementwise ops. Weight types are ggml's numbers
+ * (quant.rs:35-49): BCHIP_GGML_F32 0, F16 1, Q4_0 2, Q4_1 3, Q5_0 6, Q5_1 7, Q8_0 8,
+ * Q4K 12, Q5K 13, Q6K 14, BF16 30. */
+#define BCHIP_GGML_F32 0u
+#define BCHIP_GGML_F16 1u
+#define BCHIP_GGML_Q4_0 2u
+#define BCHIP_GGML_Q4_1 3u
+#define BCHIP_GGML_Q5_0 6u
+#define BCHIP_GGML_Q5_1 7u
+#define BCHIP_GGML_Q8_0 8u
+#define BCHIP_GGML_Q4K 12u
+#define BCHIP_GGML_Q5K 13u
+#define BCHIP_GGML_Q6K 14u
+#define BCHIP_GGML_BF16 30u
+
+/* k_matmul (kernels.h:189-214, entry cuda.cu:77-79; Gpu::matmul / matmul_rows,
+ * gpu/mod.rs:158-178): out[i][r] = sum_c W[r][c] x[i][c] for i < n, r < rows. w holds the
+ * weight matrix as stored (rows of whole ggml blocks of `type`, row stride
+ * cols / block_weights * block_bytes: matmul_rows passes its first `rows` rows only);
+ * x [n][cols] and out [n][rows] f32. cols must be a multiple of 32 (256 for the K-quants);
+ * w and x 16-byte aligned. An input row's result does not depend on n, and reruns give the
+ * same bits. */
+int bchip_matmul(bchip_ctx* ctx, const void* w, uint32_t type, const float* x, float* out,
+                 uint32_t rows, uint32_t cols, uint32_t n);
+
+/* k_rms_norm (kernels.h:216-225, entry cuda.cu:80; mod.rs:455, 485): for each of rows
+ * rows of cols, out = x / sqrt(mean(x^2) + eps) * w (w [cols]). */
+int bchip_rms_norm(bchip_ctx* ctx, const float* x, const float* w, float* out, uint32_t rows,
+                   uint32_t cols, float eps);
+
+/* k_bias_add (kernels.h:328, entry cuda.cu:86; mod.rs:459-463): x[i] += b[i % dim], i < n. */
+int bchip_bias_add(bchip_ctx* ctx, float* x, const float* b, uint64_t n, uint32_t dim);
+
+/* k_silu_mul (kernels.h:329, entry cuda.cu:87; mod.rs:488): g[i] = g[i] / (1 + e^-g[i]) * u[i]. */
+int bchip_silu_mul(bchip_ctx* ctx, float* g, const float* u, uint64_t n);
+
+/* k_add (kernels.h:330, entry cuda.cu:88; mod.rs:484, 490): x[i] += y[i], i < n. */
+int bchip_add(bchip_ctx* ctx, float* x, const float* y, uint64_t n);
 
 /* Seeded N(0,1) draws into dst (n elements of type): splitmix64 (Steele, Lea and Flood
  * 2014) + Box-Muller (1958), the generator of the benchmark inputs; draw i of seed s is

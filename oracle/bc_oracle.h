@@ -82,6 +82,43 @@ uint64_t bco_splitmix64(uint64_t* state);
 /* n N(0,1) draws from seed: pairs by Box-Muller on two splitmix64 uniforms. */
 void bco_normal(uint64_t seed, float* out, size_t n);
 
+/* ---- The rest of the layer (bc_layer.c): TEST INFRASTRUCTURE as above. ----
+ *   bcl_block, bcl_dequant_block  crates/bc-infer/src/quant.rs:69-82, 150-259
+ *   bcl_scale_min_k4              crates/bc-infer/src/quant.rs:136-146
+ *   bcl_ref_f32_to_f16            crates/bc-infer/src/quant.rs:114-131
+ *   bcl_random_tensor             crates/bc-infer/src/fixtures.rs:66-92
+ *   bcl_quantize_q8_0             crates/bc-infer/src/quant.rs:634-646
+ *   bcl_matmul_f64                crates/bc-infer/src/gpu/mod.rs:193-196 (self_check's f64 sum)
+ *   bcl_rms_norm                  crates/bc-infer/src/model.rs:381-388
+ *   bcl_silu_mul, bcl_bias_add, bcl_add   model.rs:343, 371-377, 337
+ * Pinned by tests/test_oracle.py against the reference's known-answer block tests
+ * (quant.rs:650-729), hand-built blocks of every format and numpy restatements. */
+/* ggml type numbers (quant.rs:35-49). */
+#define BCL_F32 0u
+#define BCL_F16 1u
+#define BCL_Q4_0 2u
+#define BCL_Q4_1 3u
+#define BCL_Q5_0 6u
+#define BCL_Q5_1 7u
+#define BCL_Q8_0 8u
+#define BCL_Q4K 12u
+#define BCL_Q5K 13u
+#define BCL_Q6K 14u
+#define BCL_BF16 30u
+int bcl_block(uint32_t ty, uint32_t* weights, uint32_t* bytes);
+uint16_t bcl_ref_f32_to_f16(float x);
+void bcl_scale_min_k4(uint32_t j, const uint8_t* q, float* sc, float* mn);
+void bcl_dequant_block(uint32_t ty, const uint8_t* src, float* dst);
+int bcl_dequant(uint32_t ty, const uint8_t* data, uint64_t rows, uint64_t cols, float* out);
+int bcl_random_tensor(uint32_t ty, uint64_t rows, uint64_t cols, uint64_t seed, uint8_t* out);
+void bcl_quantize_q8_0(const float* v, uint64_t n, uint8_t* out);
+int bcl_matmul_f64(uint32_t ty, const uint8_t* data, uint64_t rows, uint64_t cols, const float* x, uint64_t n,
+                   double* out);
+void bcl_rms_norm(const float* x, const float* w, float* out, uint64_t rows, uint64_t cols, float eps);
+void bcl_silu_mul(float* g, const float* u, uint64_t n);
+void bcl_bias_add(float* x, const float* b, uint64_t n, uint64_t dim);
+void bcl_add(float* x, const float* y, uint64_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,23 @@ def lib() -> ctypes.CDLL:
         L.bco_splitmix64.argtypes = [P]
         L.bco_splitmix64.restype = u64
         L.bco_normal.argtypes = [u64, P, sz]
+        L.bcl_block.argtypes = [u32, P, P]
+        L.bcl_block.restype = ctypes.c_int
+        L.bcl_ref_f32_to_f16.argtypes = [f32]
+        L.bcl_ref_f32_to_f16.restype = ctypes.c_uint16
+        L.bcl_scale_min_k4.argtypes = [u32, P, P, P]
+        L.bcl_dequant_block.argtypes = [u32, P, P]
+        L.bcl_dequant.argtypes = [u32, P, u64, u64, P]
+        L.bcl_dequant.restype = ctypes.c_int
+        L.bcl_random_tensor.argtypes = [u32, u64, u64, u64, P]
+        L.bcl_random_tensor.restype = ctypes.c_int
+        L.bcl_quantize_q8_0.argtypes = [P, u64, P]
+        L.bcl_matmul_f64.argtypes = [u32, P, u64, u64, P, u64, P]
+        L.bcl_matmul_f64.restype = ctypes.c_int
+        L.bcl_rms_norm.argtypes = [P, P, P, u64, u64, f32]
+        L.bcl_silu_mul.argtypes = [P, P, u64]
+        L.bcl_bias_add.argtypes = [P, P, u64, u64]
+        L.bcl_add.argtypes = [P, P, u64]
         _lib = L
     return _lib
 
@@ -162,3 +179,120 @@ def normal(seed: int, n: int) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().bco_normal(seed, _p(out), n)
     return out
+
+
+# ---- The rest of the layer (bc_layer.c). ----
+# ggml type numbers (quant.rs:35-49).
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4K, Q5K, Q6K, BF16 = 0, 1, 2, 3, 6, 7, 8, 12, 13, 14, 30
+GGML_TYPES = (F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4K, Q5K, Q6K)
+TYPE_NAMES = {F32: "F32", F16: "F16", BF16: "BF16", Q4_0: "Q4_0", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1",
+              Q8_0: "Q8_0", Q4K: "Q4K", Q5K: "Q5K", Q6K: "Q6K"}
+
+
+def block(ty: int) -> tuple[int, int]:
+    """quant.rs:69-82: (weights, bytes) per block."""
+    n, b = np.zeros(1, np.uint32), np.zeros(1, np.uint32)
+    if not lib().bcl_block(ty, _p(n), _p(b)):
+        raise ValueError(f"ggml type {ty}")
+    return int(n[0]), int(b[0])
+
+
+def row_bytes(ty: int, cols: int) -> int:
+    n, b = block(ty)
+    assert cols % n == 0
+    return cols // n * b
+
+
+def f16_to_f32(h: int) -> np.float32:
+    """quant.rs:93-112 (IEEE binary16 to f32, exact)."""
+    return np.float32(lib().bco_f16_to_f32(int(h)))
+
+
+def ref_f32_to_f16(x: float) -> int:
+    """quant.rs:114-131 (half up, subnormals flushed)."""
+    return int(lib().bcl_ref_f32_to_f16(float(x)))
+
+
+def scale_min_k4(j: int, q) -> tuple[float, float]:
+    """quant.rs:136-146."""
+    qb = np.ascontiguousarray(q, dtype=np.uint8)
+    sc, mn = np.zeros(1, np.float32), np.zeros(1, np.float32)
+    lib().bcl_scale_min_k4(j, _p(qb), _p(sc), _p(mn))
+    return float(sc[0]), float(mn[0])
+
+
+def dequant_block(ty: int, src) -> np.ndarray:
+    """quant.rs:150-259."""
+    n, b = block(ty)
+    sb = np.ascontiguousarray(src, dtype=np.uint8)
+    assert sb.size >= b
+    out = np.zeros(n, np.float32)
+    lib().bcl_dequant_block(ty, _p(sb), _p(out))
+    return out
+
+
+def dequant(ty: int, data, rows: int, cols: int) -> np.ndarray:
+    """quant.rs:349-362: the tensor as f32 rows."""
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    assert d.size == rows * row_bytes(ty, cols)
+    out = np.zeros((rows, cols), np.float32)
+    assert lib().bcl_dequant(ty, _p(d), rows, cols, _p(out)) == 0
+    return out
+
+
+def random_tensor(ty: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """fixtures.rs:66-92: the tensor's bytes (rows x row_bytes)."""
+    out = np.zeros(rows * row_bytes(ty, cols), np.uint8)
+    assert lib().bcl_random_tensor(ty, rows, cols, seed, _p(out)) == 0
+    return out
+
+
+def quantize_q8_0(values) -> np.ndarray:
+    """quant.rs:634-646."""
+    v = _f32(values)
+    assert v.size % 32 == 0
+    out = np.zeros(v.size // 32 * 34, np.uint8)
+    lib().bcl_quantize_q8_0(_p(v), v.size, _p(out))
+    return out
+
+
+def matmul_f64(ty: int, data, rows: int, cols: int, x, n: int) -> np.ndarray:
+    """gpu/mod.rs:193-196: out[i][r] = sum_c W[r][c] x[i][c] in f64 over dequantized weights,
+    for the first `rows` weight rows; returns [n][rows] float64."""
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    xv = _f32(x)
+    assert xv.size == n * cols
+    out = np.zeros((n, rows), np.float64)
+    assert lib().bcl_matmul_f64(ty, _p(d), rows, cols, _p(xv), n, _p(out)) == 0
+    return out
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """model.rs:381-388; x [rows][cols], w [cols]."""
+    w = _f32(w)
+    xv = _f32(x).reshape(-1, w.size)
+    out = np.zeros_like(xv)
+    lib().bcl_rms_norm(_p(xv), _p(w), _p(out), xv.shape[0], w.size, float(eps))
+    return out
+
+
+def silu_mul(g, u) -> np.ndarray:
+    """model.rs:343."""
+    gv = _f32(g).copy()
+    lib().bcl_silu_mul(_p(gv), _p(_f32(u)), gv.size)
+    return gv
+
+
+def bias_add(x, b) -> np.ndarray:
+    """model.rs:371-377."""
+    xv = _f32(x).copy()
+    bv = _f32(b)
+    lib().bcl_bias_add(_p(xv), _p(bv), xv.size, bv.size)
+    return xv
+
+
+def add(x, y) -> np.ndarray:
+    """model.rs:337."""
+    xv = _f32(x).copy()
+    lib().bcl_add(_p(xv), _p(_f32(y)), xv.size)
+    return xv
