@@ -303,6 +303,57 @@ def bench_copy_calibration(ctx, hip, mib=256, reps=4):
             "copy_GBps": 2 * n * 2 * reps / (ms * 1e-3) / 1e9}
 
 
+def synthetic_weights(wtype, rows, cols, seed):
+    """Random ggml blocks with finite, modest scales (every scale field 1/1024), as bytes."""
+    n, size = bchip.GGML_BLOCKS[wtype]
+    rng = np.random.default_rng(seed)
+    data = rng.integers(0, 256, rows * cols // n * size, dtype=np.uint8).reshape(-1, size)
+    if wtype in (bchip.GGML_F16, bchip.GGML_BF16, bchip.GGML_F32):
+        vals = rng.standard_normal(rows * cols).astype(np.float32)
+        if wtype == bchip.GGML_F16:
+            return vals.astype(np.float16).view(np.uint8)
+        if wtype == bchip.GGML_BF16:
+            return (vals.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+        return vals.view(np.uint8)
+    scale = np.frombuffer(np.float16(1.0 / 1024).tobytes(), np.uint8)
+    fields = [208] if wtype == bchip.GGML_Q6K else [0, 2] if wtype in (bchip.GGML_Q4_1, bchip.GGML_Q5_1,
+                                                                        bchip.GGML_Q4K, bchip.GGML_Q5K) else [0]
+    for f in fields:
+        data[:, f:f + 2] = scale
+    return data.reshape(-1)
+
+
+def bench_products(ctx, reps=20):
+    """The GGUF block-format product (bchip_matmul) on Llama-3-8B's largest per-layer shapes:
+    the FFN gate/up (14336 x 4096) and down (4096 x 14336) matrices, decode (one input row) and
+    an 8-row batch, in the formats real GGUF files use. Weight bytes per call / call time
+    (back-to-back calls on the stream, so launch gaps included) against 8 TB/s."""
+    out = {}
+    shapes = (("gate_14336x4096", 14336, 4096), ("down_4096x14336", 4096, 14336))
+    for wtype, name in ((bchip.GGML_Q4K, "Q4K"), (bchip.GGML_Q6K, "Q6K"), (bchip.GGML_Q8_0, "Q8_0"),
+                        (bchip.GGML_F16, "F16")):
+        for shape, rows, cols in shapes:
+            data = synthetic_weights(wtype, rows, cols, rows + cols + wtype)
+            wb = ctx.upload(data)
+            for n in (1, 8):
+                xb = ctx.upload(np.random.default_rng(n).standard_normal((n, cols)).astype(np.float32))
+                ob = ctx.zeros(n * rows * 4)
+                ctx.matmul(wb, wtype, xb, ob, rows, cols, n)
+                ctx.sync()
+                ctx.timer_start()
+                for _ in range(reps):
+                    ctx.matmul(wb, wtype, xb, ob, rows, cols, n)
+                ms = ctx.timer_stop()
+                us = ms * 1e3 / reps
+                gbps = data.nbytes / (us * 1e-6) / 1e9
+                out[f"{name}_{shape}_n{n}"] = {"weight_bytes": int(data.nbytes), "call_us": us, "GBps": gbps,
+                                              "hbm_frac": gbps / HBM_PEAK_GBS}
+                xb.free()
+                ob.free()
+            wb.free()
+    return out
+
+
 def cpu_baseline(layers=5, ctx_len=32768, nh=32, nkv=8, hd=128):
     """The oracle's single-thread attention (+ rope of the new q and k rows) per layer of one
     decode token at ctx_len slots; median over `layers` layers, scaled to 32 layers."""
@@ -359,13 +410,15 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ctx", type=int, default=32768, help="visible slots of the headline decode")
-    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,ragged,calib,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,ragged,calib,"
+                                               "products,cpu")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build runs on one GPU; the attention path's "
                                    "split over several GPUs (by KV head or by sequence chunk) is a design, not run here"}))
         sys.exit(2)
-    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "ragged", "calib", "cpu"}
+    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "ragged", "calib",
+                                                         "products", "cpu"}
     hip = Hip()
     extra = {}
     with bchip.Ctx(0) as ctx:
@@ -403,6 +456,10 @@ def main():
             log("ragged: 16 Qwen2.5-7B sequences, 28 layers")
             extra["ragged_qwen7b"] = bench_ragged(ctx, hip, 5)
             log(json.dumps(extra["ragged_qwen7b"]))
+        if "products" in want:
+            log("GGUF block-format products at Llama-3-8B FFN shapes (the rest of the layer)")
+            extra["products"] = bench_products(ctx)
+            log(json.dumps(extra["products"]))
     cpu = None
     if "cpu" in want:
         log("cpu baseline (oracle, 1 thread)")

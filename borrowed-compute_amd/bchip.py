@@ -20,6 +20,17 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "bchip.h")
 F32, F16 = 0, 1
 OK, E_ARG, E_HIP, E_NODEV, E_DISABLED, E_UNSUPPORTED, E_OOM = 0, -1, -2, -3, -4, -5, -6
 CHUNK_MULTI = 192
+# ggml weight types (quant.rs:35-49) and (weights, bytes) per block (quant.rs:69-82).
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_1, GGML_Q5_0, GGML_Q5_1, GGML_Q8_0 = 0, 1, 2, 3, 6, 7, 8
+GGML_Q4K, GGML_Q5K, GGML_Q6K, GGML_BF16 = 12, 13, 14, 30
+GGML_BLOCKS = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_BF16: (1, 2), GGML_Q4_0: (32, 18), GGML_Q4_1: (32, 20),
+               GGML_Q5_0: (32, 22), GGML_Q5_1: (32, 24), GGML_Q8_0: (32, 34), GGML_Q4K: (256, 144),
+               GGML_Q5K: (256, 176), GGML_Q6K: (256, 210)}
+
+
+def ggml_row_bytes(wtype: int, cols: int) -> int:
+    n, b = GGML_BLOCKS[wtype]
+    return cols // n * b
 
 _lib = None
 

@@ -5,11 +5,11 @@
 // Product layout: weights stay in their ggml blocks, rows of whole blocks (row_bytes =
 // cols / block_weights * block_bytes); every format is read a "group" of 32 weights at a
 // time. A wave owns ROWS_PER_WAVE weight rows and its 64 lanes take groups l, l + 64, ...
-// of them: per group the lane loads its input values once (up to NB input rows) and
-// dequantizes each of its rows' 32 weights once, with quant.rs's per-weight expression, then
-// sums weight x input in a fixed order. The 64 lane sums meet in a fixed butterfly. So an
-// input row's result depends on that row alone, never on how many rows share the batch,
-// and reruns give the same bits (the reference kernel's properties, kernels.h:9-11).
+// of them: per group the lane loads its input values once (up to NB input rows), unpacks
+// each of its rows' 32 quants once, and sums in a fixed order. The 64 lane sums meet in a
+// fixed butterfly. So an input row's result depends on that row alone, never on how many
+// rows share the batch, and reruns give the same bits (the reference kernel's properties,
+// kernels.h:9-11).
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -61,17 +61,33 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, const uint8_t* q, float
     }
 }
 
-// The 32 weights of group g of a stored row, w[j] = weight 32g + j, each by its format's
-// expression in quant.rs:150-259 (same association, so each weight has the bits the CPU's
-// dequantization gives it).
+// Group g of a stored row as its quants and per-half affine maps: weight j = a[h] * q[j] +
+// b[h] for h = j / 16 (quant.rs:150-259's values: Q4_0 (q - 8) d, Q4_1 q d + m, Q5_0
+// (q - 16) d, Q5_1 q d + m, Q8_0 q d, Q4K/Q5K ds q - dm, Q6K d_h (q - 32); the plain types
+// are their values with a = 1, b = 0). The product then needs per half only sum(q x) and
+// sum(x): one conversion and one FMA a weight, not a dequantization and a product.
 template <uint32_t TY>
-__device__ __forceinline__ void group_weights(const uint8_t* __restrict__ row, uint32_t g, float (&w)[32]) {
+constexpr bool plain_type() {
+    return TY == G_F32 || TY == G_F16 || TY == G_BF16;
+}
+
+// Bytes 0..3 of v as floats (the hardware's byte-to-float conversions).
+__device__ __forceinline__ void bytes4(uint32_t v, float* q) {
+    q[0] = (float)(v & 255u);
+    q[1] = (float)((v >> 8) & 255u);
+    q[2] = (float)((v >> 16) & 255u);
+    q[3] = (float)(v >> 24);
+}
+
+template <uint32_t TY>
+__device__ __forceinline__ void group_quants(const uint8_t* __restrict__ row, uint32_t g, float (&q)[32],
+                                             float (&a)[2], float (&b)[2]) {
     if constexpr (TY == G_F32) {
         const float4* p = (const float4*)(row + (size_t)g * 128);
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const float4 v = p[k];
-            w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+            q[4 * k] = v.x; q[4 * k + 1] = v.y; q[4 * k + 2] = v.z; q[4 * k + 3] = v.w;
         }
     } else if constexpr (TY == G_F16 || TY == G_BF16) {
         const uint4* p = (const uint4*)(row + (size_t)g * 64);
@@ -82,109 +98,88 @@ __device__ __forceinline__ void group_weights(const uint8_t* __restrict__ row, u
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 if constexpr (TY == G_F16) {
-                    w[8 * k + 2 * j] = h2f(u[j] & 0xffffu);
-                    w[8 * k + 2 * j + 1] = h2f(u[j] >> 16);
+                    q[8 * k + 2 * j] = h2f(u[j] & 0xffffu);
+                    q[8 * k + 2 * j + 1] = h2f(u[j] >> 16);
                 } else {
-                    w[8 * k + 2 * j] = __uint_as_float(u[j] << 16);
-                    w[8 * k + 2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+                    q[8 * k + 2 * j] = __uint_as_float(u[j] << 16);
+                    q[8 * k + 2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
                 }
             }
         }
-    } else if constexpr (TY == G_Q4_0 || TY == G_Q5_0 || TY == G_Q8_0) {
-        // 2-byte-aligned blocks: 16-bit loads.
-        const uint8_t* b = row + (size_t)g * (TY == G_Q4_0 ? 18 : TY == G_Q5_0 ? 22 : 34);
-        const float d = h2f(ld16(b));
-        if constexpr (TY == G_Q8_0) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint32_t v = ld32h(b + 2 + 4 * k);
-#pragma unroll
-                for (int j = 0; j < 4; j++) w[4 * k + j] = i8f(v >> (8 * j)) * d;
-            }
-        } else {
-            const uint8_t* qs = b + (TY == G_Q4_0 ? 2 : 6);
-            const uint32_t qh = TY == G_Q5_0 ? ld32h(b + 2) : 0u;
-            const float off = TY == G_Q4_0 ? 8.0f : 16.0f;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t v = ld32h(qs + 4 * k);
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t e = 4 * k + j, byte = (v >> (8 * j)) & 255u;
-                    uint32_t lo = byte & 15u, hi = byte >> 4;
-                    if constexpr (TY == G_Q5_0) {
-                        lo |= ((qh >> e) << 4) & 16u;
-                        hi |= (qh >> (e + 12)) & 16u;
-                    }
-                    // Q5_0 adds its zero minimum as quant.rs does (-0 becomes +0).
-                    w[e] = TY == G_Q5_0 ? ((float)lo - off) * d + 0.0f : ((float)lo - off) * d;
-                    w[e + 16] = TY == G_Q5_0 ? ((float)hi - off) * d + 0.0f : ((float)hi - off) * d;
-                }
-            }
-        }
-    } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
-        const uint8_t* b = row + (size_t)g * (TY == G_Q4_1 ? 20 : 24);
-        const uint32_t dm = ld32(b);
-        const float d = h2f(dm & 0xffffu), m = h2f(dm >> 16);
-        const uint8_t* qs = b + (TY == G_Q4_1 ? 4 : 8);
-        const uint32_t qh = TY == G_Q5_1 ? ld32(b + 4) : 0u;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t v = ld32(qs + 4 * k);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t e = 4 * k + j, byte = (v >> (8 * j)) & 255u;
-                uint32_t lo = byte & 15u, hi = byte >> 4;
-                if constexpr (TY == G_Q5_1) {
-                    lo |= ((qh >> e) << 4) & 16u;
-                    hi |= (qh >> (e + 12)) & 16u;
-                }
-                w[e] = (float)lo * d + m;
-                w[e + 16] = (float)hi * d + m;
-            }
-        }
-    } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
-        // 256 weights a block in 4 chunks of 64: group 2c is chunk c's low nibbles, 2c + 1 its
-        // high nibbles.
-        const uint8_t* b = row + (size_t)(g / 8) * (TY == G_Q4K ? 144 : 176);
-        const uint32_t sub = g % 8, c = sub / 2, hi = sub % 2;
-        const uint32_t dd = ld32(b);
-        const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
-        float sc, mn;
-        scale_min_k4(sub, b + 4, sc, mn);
-        const float ds = d * sc, dm = dmin * mn;
-        const uint8_t* qs = b + (TY == G_Q4K ? 16 : 48) + 32 * c;
+    } else if constexpr (TY == G_Q8_0) {
+        const uint8_t* b8 = row + (size_t)g * 34;
+        const float d = h2f(ld16(b8));
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const uint32_t v = ld32(qs + 4 * k);
-            const uint32_t h = TY == G_Q5K ? ld32(b + 16 + 4 * k) : 0u;
+            const uint32_t v = ld32h(b8 + 2 + 4 * k);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                uint32_t q = (v >> (8 * j + 4 * hi)) & 15u;
-                if constexpr (TY == G_Q5K) q += ((h >> (8 * j + 2 * c + hi)) & 1u) << 4;
-                w[4 * k + j] = ds * (float)q - dm;
-            }
+            for (int j = 0; j < 4; j++) q[4 * k + j] = i8f(v >> (8 * j));
         }
+        a[0] = a[1] = d;
+        b[0] = b[1] = 0.0f;
+    } else if constexpr (TY == G_Q4_0 || TY == G_Q5_0 || TY == G_Q4_1 || TY == G_Q5_1) {
+        // 16 bytes: element j in byte j's low nibble, j + 16 in its high nibble; Q5 adds bit j
+        // of qh as bit 4 of element j.
+        constexpr bool Q41 = TY == G_Q4_1 || TY == G_Q5_1, FIVE = TY == G_Q5_0 || TY == G_Q5_1;
+        constexpr uint32_t BS = TY == G_Q4_0 ? 18 : TY == G_Q4_1 ? 20 : TY == G_Q5_0 ? 22 : 24;
+        const uint8_t* bb = row + (size_t)g * BS;
+        const float d = h2f(ld16(bb));
+        const float m = Q41 ? h2f(ld16(bb + 2)) : 0.0f;
+        const uint32_t qh = FIVE ? ld32h(bb + (Q41 ? 4 : 2)) : 0u;
+        const uint8_t* qs = bb + (Q41 ? 4 : 2) + (FIVE ? 4 : 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t v = Q41 ? ld32(qs + 4 * k) : ld32h(qs + 4 * k);
+            uint32_t lo = v & 0x0f0f0f0fu, hi = (v >> 4) & 0x0f0f0f0fu;
+            if constexpr (FIVE) {
+                // bits 4k .. 4k+3 of qh to bit 4 of bytes 0..3; bits 16 + 4k .. likewise
+                const uint32_t l4 = (qh >> (4 * k)) & 15u, h4 = (qh >> (16 + 4 * k)) & 15u;
+                lo |= ((l4 & 1u) << 4) | ((l4 & 2u) << 11) | ((l4 & 4u) << 18) | ((l4 & 8u) << 25);
+                hi |= ((h4 & 1u) << 4) | ((h4 & 2u) << 11) | ((h4 & 4u) << 18) | ((h4 & 8u) << 25);
+            }
+            bytes4(lo, &q[4 * k]);
+            bytes4(hi, &q[16 + 4 * k]);
+        }
+        a[0] = a[1] = d;
+        b[0] = b[1] = Q41 ? m : (TY == G_Q4_0 ? -8.0f : -16.0f) * d;
+    } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
+        // 256 weights a block in 4 chunks of 64: group 2c is chunk c's low nibbles, 2c + 1 its
+        // high nibbles (Q5K: plus bit 2c + hi of each qh byte, as bit 4).
+        const uint8_t* bb = row + (size_t)(g / 8) * (TY == G_Q4K ? 144 : 176);
+        const uint32_t sub = g % 8, c = sub / 2, hi = sub % 2;
+        const uint32_t dd = ld32(bb);
+        const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
+        float sc, mn;
+        scale_min_k4(sub, bb + 4, sc, mn);
+        const uint8_t* qs = bb + (TY == G_Q4K ? 16 : 48) + 32 * c;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            uint32_t v = (ld32(qs + 4 * k) >> (4 * hi)) & 0x0f0f0f0fu;
+            if constexpr (TY == G_Q5K) v |= ((ld32(bb + 16 + 4 * k) >> (2 * c + hi)) & 0x01010101u) << 4;
+            bytes4(v, &q[4 * k]);
+        }
+        a[0] = a[1] = d * sc;
+        b[0] = b[1] = -(dmin * mn);
     } else if constexpr (TY == G_Q6K) {
         // Half hh, quarter qr of a 256-block: ql bytes 64hh + 32(qr % 2) .., nibble qr / 2;
         // qh bytes 128 + 32hh .., bits 2qr; scales 192 + 8hh + 2qr (+1 for weights 16..31).
-        const uint8_t* b = row + (size_t)(g / 8) * 210;
+        const uint8_t* bb = row + (size_t)(g / 8) * 210;
         const uint32_t sub = g % 8, hh = sub / 4, qr = sub % 4;
-        const uint8_t* ql = b + 64 * hh + ((qr & 1u) ? 32 : 0);
-        const uint8_t* qh = b + 128 + 32 * hh;
-        const float d = h2f(ld16(b + 208));
-        const uint32_t scs = ld16(b + 192 + 8 * hh + 2 * qr);
-        const float d0 = d * i8f(scs & 255u), d1 = d * i8f(scs >> 8);
+        const uint8_t* ql = bb + 64 * hh + ((qr & 1u) ? 32 : 0);
+        const uint8_t* qh = bb + 128 + 32 * hh;
+        const float d = h2f(ld16(bb + 208));
+        const uint32_t scs = ld16(bb + 192 + 8 * hh + 2 * qr);
         const uint32_t shift = qr < 2 ? 0 : 4;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const uint32_t lo = ld32h(ql + 4 * k), h = ld32h(qh + 4 * k);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int q = (int)(((lo >> (8 * j + shift)) & 15u) | (((h >> (8 * j + 2 * qr)) & 3u) << 4)) - 32;
-                w[4 * k + j] = (k < 4 ? d0 : d1) * (float)q;
-            }
+            const uint32_t v = ((ld32h(ql + 4 * k) >> shift) & 0x0f0f0f0fu) |
+                               (((ld32h(qh + 4 * k) >> (2 * qr)) & 0x03030303u) << 4);
+            bytes4(v, &q[4 * k]);
         }
+        a[0] = d * i8f(scs & 255u);
+        a[1] = d * i8f(scs >> 8);
+        b[0] = -32.0f * a[0];
+        b[1] = -32.0f * a[1];
     }
 }
 
@@ -203,13 +198,23 @@ struct MatmulParams {
 };
 
 // out[i][r] = sum_c W[r][c] x[i][c]: workgroup (blockIdx.x) = MM_WAVES waves x ROWS_PER_WAVE
-// weight rows, blockIdx.y = input rows i0 .. i0 + NB.
+// weight rows, blockIdx.y = input rows i0 .. i0 + NB. The input rows pass through LDS in
+// column tiles of 64 groups (one group a lane), read from HBM once per workgroup with
+// coalesced loads and stored with a padded group stride (XS floats) so that each lane's
+// 16-byte reads of its group fall on distinct banks. Per lane, group and input row: the two
+// half sums of q x (FMA chains, weights in order) and of x, then
+// acc += a0 sq0 + a1 sq1 + b0 sx0 + b1 sx1 (in that order, as FMAs).
+constexpr int XS = 36;              // LDS floats per group of 32 inputs
+constexpr int TILE_GROUPS = 64;     // groups per column tile: one per lane
+
 template <uint32_t TY>
 __global__ __launch_bounds__(64 * MM_WAVES) void k_matmul(const MatmulParams p) {
+    // nb tiles of TILE_GROUPS * XS floats (dynamic: a one-row pass takes 9 KB, so more
+    // workgroups share a CU).
+    extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t r0 = (blockIdx.x * MM_WAVES + wave) * ROWS_PER_WAVE;
-    if (r0 >= p.rows) return;
     const uint32_t i0 = blockIdx.y * NB;
     const uint32_t nb = min((uint32_t)NB, p.n - i0);
     const uint32_t groups = p.cols / 32;
@@ -218,31 +223,64 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_matmul(const MatmulParams p) 
     for (int i = 0; i < NB; i++)
 #pragma unroll
         for (int r = 0; r < ROWS_PER_WAVE; r++) acc[i][r] = 0.0f;
-    // Rows past the matrix read row r0 again (their sums are never stored).
+    // Rows past the matrix read its last row (their sums are never stored).
     const uint8_t* rowp[ROWS_PER_WAVE];
 #pragma unroll
     for (int r = 0; r < ROWS_PER_WAVE; r++)
-        rowp[r] = p.w + (size_t)(r0 + r < p.rows ? r0 + r : r0) * p.row_bytes;
-    for (uint32_t g = lane; g < groups; g += 64) {
-        float w[ROWS_PER_WAVE][32];
+        rowp[r] = p.w + (size_t)min(r0 + r, p.rows - 1) * p.row_bytes;
+    for (uint32_t t0 = 0; t0 < groups; t0 += TILE_GROUPS) {
+        const uint32_t tg = min((uint32_t)TILE_GROUPS, groups - t0);
+        // This lane's weights first (their loads then overlap the input tile's), lanes past
+        // the tile reading its first group; then the tile of every input row: float4 e of it
+        // is group e / 8, quarter e % 8.
+        const uint32_t g = t0 + (lane < tg ? lane : 0u);
+        float q[ROWS_PER_WAVE][32], a[ROWS_PER_WAVE][2], b[ROWS_PER_WAVE][2];
 #pragma unroll
-        for (int r = 0; r < ROWS_PER_WAVE; r++) group_weights<TY>(rowp[r], g, w[r]);
+        for (int r = 0; r < ROWS_PER_WAVE; r++) group_quants<TY>(rowp[r], g, q[r], a[r], b[r]);
+        __syncthreads();
+        for (uint32_t e = threadIdx.x; e < nb * tg * 8; e += 64 * MM_WAVES) {
+            const uint32_t i = e / (tg * 8), f = e % (tg * 8);
+            const float4 v = *(const float4*)(p.x + (size_t)(i0 + i) * p.cols + 32 * t0 + 4 * f);
+            *(float4*)&xs_dyn[i * TILE_GROUPS * XS + (f / 8) * XS + 4 * (f % 8)] = v;
+        }
+        __syncthreads();
+        if (lane >= tg) continue;
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             if (i < (int)nb) {
-                const float4* xg = (const float4*)(p.x + (size_t)(i0 + i) * p.cols + 32 * g);
                 float xv[32];
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
-                    const float4 v = xg[k];
+                    const float4 v = *(const float4*)&xs_dyn[i * TILE_GROUPS * XS + lane * XS + 4 * k];
                     xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
+                }
+                float sx0 = 0.0f, sx1 = 0.0f;
+                if constexpr (!plain_type<TY>()) {
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        sx0 += xv[j];
+                        sx1 += xv[16 + j];
+                    }
                 }
 #pragma unroll
                 for (int r = 0; r < ROWS_PER_WAVE; r++) {
-                    float s = 0.0f;
+                    if constexpr (plain_type<TY>()) {
+                        float s = acc[i][r];
 #pragma unroll
-                    for (int j = 0; j < 32; j++) s += w[r][j] * xv[j];
-                    acc[i][r] += s;
+                        for (int j = 0; j < 32; j++) s = __builtin_fmaf(q[r][j], xv[j], s);
+                        acc[i][r] = s;
+                    } else {
+                        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < 16; j++) {
+                            s0 = __builtin_fmaf(q[r][j], xv[j], s0);
+                            s1 = __builtin_fmaf(q[r][16 + j], xv[16 + j], s1);
+                        }
+                        float t = __builtin_fmaf(a[r][0], s0, acc[i][r]);
+                        t = __builtin_fmaf(a[r][1], s1, t);
+                        t = __builtin_fmaf(b[r][0], sx0, t);
+                        acc[i][r] = __builtin_fmaf(b[r][1], sx1, t);
+                    }
                 }
             }
         }
@@ -263,7 +301,8 @@ template <uint32_t TY>
 static hipError_t matmul_t(const MatmulParams& mp, hipStream_t s) {
     const uint32_t per_wg = MM_WAVES * ROWS_PER_WAVE;
     const dim3 grid((mp.rows + per_wg - 1) / per_wg, (mp.n + NB - 1) / NB);
-    hipLaunchKernelGGL((k_matmul<TY>), grid, dim3(64 * MM_WAVES), 0, s, mp);
+    const size_t lds = (size_t)min(mp.n, (uint32_t)NB) * TILE_GROUPS * XS * sizeof(float);
+    hipLaunchKernelGGL((k_matmul<TY>), grid, dim3(64 * MM_WAVES), lds, s, mp);
     return hipGetLastError();
 }
 
