@@ -338,6 +338,8 @@ int bchip_matmul(bchip_ctx* c, const void* w, uint32_t type, const float* x, flo
     if (cols == 0 || cols % 32 || cols % bw) return fail(BCHIP_E_ARG, "cols %u: not whole groups of 32 and blocks of %u", cols, bw);
     if ((uintptr_t)w % 16 || (uintptr_t)x % 16) return fail(BCHIP_E_ARG, "w and x must be 16-byte aligned");
     const uint64_t row_bytes = (uint64_t)cols / bw * bb;
+    if (row_bytes > UINT32_MAX) return fail(BCHIP_E_ARG, "cols %u: a row of more than 4 GiB", cols);
+    if (n > MATMUL_MAX_N) return fail(BCHIP_E_ARG, "%u input rows (at most %u a call)", n, MATMUL_MAX_N);
     CHECK(check_span(c, w, row_bytes * rows, "weights"));
     CHECK(check_span(c, x, (uint64_t)n * cols * 4, "x"));
     CHECK(check_span(c, out, (uint64_t)n * rows * 4, "out"));

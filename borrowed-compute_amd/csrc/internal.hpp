@@ -76,6 +76,8 @@ hipError_t fill_normal_launch(void* dst, uint32_t type, uint64_t n, uint64_t see
 
 // The rest of a layer (layer.hip).
 bool ggml_block(uint32_t type, uint32_t& weights, uint32_t& bytes);
+// Input rows one product call takes: passes of 8 rows over the grid's y dimension (65535).
+constexpr uint32_t MATMUL_MAX_N = 8u * 65535u;
 hipError_t matmul_launch(const void* w, uint32_t type, const float* x, float* out, uint32_t rows, uint32_t cols,
                          uint32_t n, uint32_t row_bytes, hipStream_t s);
 hipError_t rms_norm_launch(const float* x, const float* w, float* out, uint32_t rows, uint32_t cols, float eps,

@@ -97,6 +97,8 @@ def test_product_refuses_bad_shapes(ctx):
         ctx.matmul(wb, O.F32, xb, ob, 1, 48, 1)  # groups of 32
     with pytest.raises(bchip.BchipError):
         ctx.matmul(wb, O.Q8_0, xb, ob, 200, 256, 1)  # weights pass the end of their buffer
+    with pytest.raises(bchip.BchipError):
+        ctx.matmul(wb, O.F32, xb, ob, 1, 32, 8 * 65535 + 1)  # more input rows than a call takes
     for b in (wb, xb, ob):
         b.free()
 
