@@ -74,6 +74,7 @@ def lib() -> ctypes.CDLL:
         "bchip_copy": ([P, P, u32, P, u32, u64, u64], i32),
         "bchip_move": ([P, P, u32, u64, u64, u64], i32),
         "bchip_keep": ([P, P, u32, u32, u32, u64, P, u32], i32),
+        "bchip_cache_grow": ([P, P, P, u32, u32, u64, u64], i32),
         "bchip_rope_append": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, u64], i32),
         "bchip_attention": ([P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32], i32),
         "bchip_rope_append_attention": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32, P], i32),
@@ -204,6 +205,12 @@ class Ctx:
         r = np.ascontiguousarray(rows, np.uint32)
         check(lib().bchip_keep(self.h, arr, len(bufs), t, width, base, r.ctypes.data_as(ctypes.c_void_p), len(r)))
 
+    def cache_grow(self, srcs, dsts, t, keep, total) -> None:
+        n = len(dsts)
+        sa = (ctypes.c_void_p * n)(*[_ptr(b) for b in srcs]) if srcs else None
+        da = (ctypes.c_void_p * n)(*[_ptr(b) for b in dsts])
+        check(lib().bchip_cache_grow(self.h, sa, da, n, t, keep, total))
+
     def rope_append(self, q, k, v, kc, vc, kv_type, inv_freq, positions, rows, nh, nkv, hd, rope_dim, neox,
                     slot0) -> None:
         check(lib().bchip_rope_append(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc), kv_type,
@@ -256,6 +263,58 @@ class Ctx:
         ms = ctypes.c_float()
         check(lib().bchip_timer_stop(self.h, ctypes.byref(ms)))
         return ms.value
+
+
+def grown_capacity(cap: int, need: int, context: int) -> int:
+    """Gpu::reserve's new capacity in tokens (gpu/mod.rs:409): what is needed, at least twice
+    the old capacity and at least 256, but no more than the context (or what is needed, when
+    that is more)."""
+    return min(max(need, cap * 2, 256), max(context, need))
+
+
+class KvCache:
+    """A model's KV cache on the device, the reference's Cache (gpu/mod.rs:300-337) with
+    Gpu::new_cache and Gpu::reserve (mod.rs:398-423): per layer a K and a V buffer of
+    cap x kvd elements of kv_type (kvd = n_head_kv * head_dim), grown by doubling, the kept
+    prefix copied for every layer in one launch (bchip_cache_grow), and Cache::keep in one
+    launch (bchip_keep)."""
+
+    def __init__(self, ctx: "Ctx", n_layer: int, kvd: int, kv_type: int = F16):
+        self.ctx, self.n_layer, self.kvd, self.kv_type = ctx, n_layer, kvd, kv_type
+        self.k: list[Buf] = []
+        self.v: list[Buf] = []
+        self.cap = 0
+
+    def reserve(self, need: int, keep: int, context: int) -> None:
+        """Grows the cache to hold `need` tokens, keeping its first `keep` (mod.rs:403-423)."""
+        if need <= self.cap:
+            return
+        if keep > self.cap:
+            raise ValueError(f"keep {keep} past the cache's {self.cap} tokens")
+        cap = grown_capacity(self.cap, need, context)
+        nbytes = cap * self.kvd * esize(self.kv_type)
+        k = [Buf(self.ctx, nbytes) for _ in range(self.n_layer)]
+        v = [Buf(self.ctx, nbytes) for _ in range(self.n_layer)]
+        old = self.k + self.v
+        if keep > 0 and old:
+            self.ctx.cache_grow(old, k + v, self.kv_type, keep * self.kvd, cap * self.kvd)
+        for b in old:
+            b.free()
+        self.k, self.v, self.cap = k, v, cap
+
+    def keep(self, base: int, rows) -> None:
+        """Cache::keep (mod.rs:322-337): the accepted rows move down to base, base + 1, ..."""
+        if self.k:
+            self.ctx.keep(self.k + self.v, self.kv_type, self.kvd, base, rows)
+
+    def bytes(self) -> int:
+        """Cache::bytes: device bytes the cache holds."""
+        return len(self.k) * 2 * self.cap * self.kvd * esize(self.kv_type)
+
+    def free(self) -> None:
+        for b in self.k + self.v:
+            b.free()
+        self.k, self.v, self.cap = [], [], 0
 
 
 def _ptr(x):

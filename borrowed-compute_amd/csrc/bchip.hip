@@ -408,6 +408,31 @@ int bchip_move(bchip_ctx* c, void* buf, uint32_t type, uint64_t from, uint64_t t
     return BCHIP_OK;
 }
 
+int bchip_cache_grow(bchip_ctx* c, const void* const* src, void* const* dst, uint32_t nbufs, uint32_t type,
+                     uint64_t keep, uint64_t total) {
+    CHECK(enter(c));
+    if (nbufs == 0 || total == 0) return BCHIP_OK;
+    if (!dst || (keep > 0 && !src)) return fail(BCHIP_E_ARG, "null pointer");
+    if (type > 1) return fail(BCHIP_E_ARG, "element type %u", type);
+    if (keep > total) return fail(BCHIP_E_ARG, "keep %llu past total %llu", (unsigned long long)keep,
+                                  (unsigned long long)total);
+    const uint64_t kb = keep * esize(type), tb = total * esize(type);
+    for (uint32_t b = 0; b < nbufs; b++) {
+        const uint8_t* s = keep > 0 ? (const uint8_t*)src[b] : nullptr;
+        const uint8_t* d = (const uint8_t*)dst[b];
+        if (!d || (keep > 0 && !s)) return fail(BCHIP_E_ARG, "null buffer %u", b);
+        if ((uintptr_t)d % 16 || (uintptr_t)s % 16) return fail(BCHIP_E_ARG, "buffer %u: not 16-byte aligned", b);
+        if (s && s < d + tb && d < s + kb) return fail(BCHIP_E_ARG, "buffer %u: source and destination overlap", b);
+        if (s) CHECK(check_span(c, s, kb, "grow source"));
+        CHECK(check_span(c, d, tb, "grow destination"));
+    }
+    std::vector<const void*> sv(nbufs, nullptr);
+    if (keep > 0)
+        for (uint32_t b = 0; b < nbufs; b++) sv[b] = src[b];
+    HIP_TRY(grow_launch(sv.data(), dst, nbufs, kb, tb, c->stream), "cache_grow");
+    return BCHIP_OK;
+}
+
 int bchip_keep(bchip_ctx* c, void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width, uint64_t base,
                const uint32_t* rows, uint32_t nrows) {
     CHECK(enter(c));

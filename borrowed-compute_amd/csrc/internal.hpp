@@ -72,6 +72,8 @@ hipError_t copy_launch(const void* src, uint32_t st, void* dst, uint32_t dt, uin
 hipError_t move_launch(void* buf, uint32_t type, uint64_t from, uint64_t to, uint64_t n, hipStream_t s);
 hipError_t keep_launch(void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width, uint64_t base,
                        const uint32_t* rows, uint32_t nrows, hipStream_t s);
+hipError_t grow_launch(const void* const* src, void* const* dst, uint32_t nbufs, uint64_t keep_bytes,
+                       uint64_t total_bytes, hipStream_t s);
 hipError_t fill_normal_launch(void* dst, uint32_t type, uint64_t n, uint64_t seed, hipStream_t s);
 
 // The rest of a layer (layer.hip).

@@ -1,6 +1,7 @@
 // KV-cache movement: bc-infer's k_copy and k_move (crates/bc-infer/src/gpu/kernels.h:332-334,
 // entries cuda.cu:89-90), f16-aware, plus Cache::keep for every layer in one launch
-// (gpu/mod.rs:322-337), and the seeded N(0,1) generator of the benchmark inputs.
+// (gpu/mod.rs:322-337), the cache growth of Gpu::reserve for every layer in one launch
+// (gpu/mod.rs:404-423), and the seeded N(0,1) generator of the benchmark inputs.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -46,6 +47,30 @@ __global__ __launch_bounds__(256) void k_keep(const KeepArgs a, uint32_t nbufs, 
     for (uint32_t i = 0; i < nrows; i++) {
         const uint32_t r = a.rows[i];
         if (r != i) b[(base + i) * width + col] = b[(base + r) * width + col];
+    }
+}
+
+struct GrowArgs {
+    const uint8_t* src[64];
+    uint8_t* dst[64];
+};
+
+// Cache growth for every layer's K and V in one launch: buffer blockIdx.y gets
+// dst[0, keep) = src[0, keep) and dst[keep, total) = 0 (bytes), 16 bytes a thread; the one
+// 16-byte piece that straddles keep goes byte by byte, so src is never read past keep.
+__global__ __launch_bounds__(256) void k_grow(const GrowArgs a, uint64_t keep, uint64_t total) {
+    const uint8_t* src = a.src[blockIdx.y];
+    uint8_t* dst = a.dst[blockIdx.y];
+    const uint64_t pieces = (total + 15) / 16;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t b0 = 16 * i;
+        if (b0 + 16 <= keep) {
+            *(uint4*)(dst + b0) = *(const uint4*)(src + b0);
+        } else if (b0 >= keep && b0 + 16 <= total) {
+            *(uint4*)(dst + b0) = uint4{0u, 0u, 0u, 0u};
+        } else {
+            for (uint64_t b = b0; b < b0 + 16 && b < total; b++) dst[b] = b < keep ? src[b] : (uint8_t)0;
+        }
     }
 }
 
@@ -119,6 +144,25 @@ hipError_t keep_launch(void* const* bufs, uint32_t nbufs, uint32_t type, uint32_
             hipLaunchKernelGGL(k_keep<f16>, g, dim3(256), 0, s, a, nb, width, base, nrows);
         else
             hipLaunchKernelGGL(k_keep<float>, g, dim3(256), 0, s, a, nb, width, base, nrows);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t grow_launch(const void* const* src, void* const* dst, uint32_t nbufs, uint64_t keep_bytes,
+                       uint64_t total_bytes, hipStream_t s) {
+    if (nbufs == 0 || total_bytes == 0) return hipSuccess;
+    for (uint32_t b0 = 0; b0 < nbufs; b0 += 64) {
+        GrowArgs a{};
+        const uint32_t nb = (nbufs - b0 < 64) ? nbufs - b0 : 64;
+        for (uint32_t i = 0; i < nb; i++) {
+            a.src[i] = (const uint8_t*)src[b0 + i];
+            a.dst[i] = (uint8_t*)dst[b0 + i];
+        }
+        const uint64_t pieces = (total_bytes + 15) / 16;
+        const uint32_t gx = (uint32_t)((pieces + 255) / 256 > 2048 ? 2048 : (pieces + 255) / 256);
+        hipLaunchKernelGGL(k_grow, dim3(gx, nb), dim3(256), 0, s, a, keep_bytes, total_bytes);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

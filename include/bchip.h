@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BCHIP_ABI_VERSION 2
+#define BCHIP_ABI_VERSION 3
 
 enum bchip_type { BCHIP_F32 = 0, BCHIP_F16 = 1 }; /* T_F32 / T_F16 of kernels.h:14-15 */
 
@@ -98,6 +98,14 @@ int bchip_move(bchip_ctx* ctx, void* buf, uint32_t type, uint64_t from, uint64_t
  * bufs is a host array of device pointers. */
 int bchip_keep(bchip_ctx* ctx, void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width,
                uint64_t base, const uint32_t* rows, uint32_t nrows);
+
+/* The copy step of Gpu::reserve (mod.rs:404-423): for each of `nbufs` pairs (every layer's
+ * K and V), dst[0, keep) = src[0, keep) and dst[keep, total) = 0, in elements of `type`,
+ * all pairs in one launch (the reference zero-allocates each new buffer, then issues one
+ * K::Copy per buffer). src and dst are host arrays of device pointers, each 16-byte
+ * aligned; a pair's ranges may not overlap; src may be NULL when keep is 0. */
+int bchip_cache_grow(bchip_ctx* ctx, const void* const* src, void* const* dst, uint32_t nbufs, uint32_t type,
+                     uint64_t keep, uint64_t total);
 
 /* The attention sub-sequence k_rope(q), k_rope(k), k_copy(k -> kc), k_copy(v -> vc)
  * (mod.rs:464-475) as one launch: rotates q [rows][nh][hd] in place, rotates k

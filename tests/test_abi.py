@@ -17,7 +17,7 @@ def test_library_exports_every_declared_function():
     assert len(names) >= 20
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.bchip_abi_version() == 2
+    assert lib.bchip_abi_version() == 3
 
 
 def test_exported_symbols_are_exactly_the_header():
@@ -55,3 +55,19 @@ def test_gpu_off_switch():
 def test_no_device_is_an_error_not_a_crash():
     rc, msg = _init_in_child({})
     assert rc in (bchip.E_NODEV, bchip.E_HIP) and msg
+
+
+def test_cache_capacity_grows_as_the_reference_reserve():
+    """Gpu::reserve (gpu/mod.rs:409): at least 256 tokens, doubling, capped by the context
+    unless one call needs more."""
+    from bchip import grown_capacity
+    assert grown_capacity(0, 10, 4096) == 256
+    assert grown_capacity(0, 300, 4096) == 300
+    assert grown_capacity(256, 257, 4096) == 512
+    assert grown_capacity(300, 400, 4096) == 600
+    assert grown_capacity(3000, 3001, 4096) == 4096
+    assert grown_capacity(4096, 5000, 4096) == 5000
+    assert grown_capacity(0, 100, 128) == 128
+    for cap, need, context in [(0, 1, 8), (256, 900, 100000), (1 << 20, (1 << 20) + 1, 1 << 22)]:
+        got = grown_capacity(cap, need, context)
+        assert got >= need and (got >= min(2 * cap, context) or got == need)
