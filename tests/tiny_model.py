@@ -1,0 +1,140 @@
+"""Test fixture: the reference's small random Llama-shaped model (crates/bc-infer/src/
+fixtures.rs:7-60), restated: width 64, feed-forward 128, vocabulary 96, 4 query and 2 KV
+heads, Q8_0 matrices (quantised by the oracle's restatement of quant.rs:634-646), f32
+norms and q bias, the weights drawn from one xorshift stream in the file's tensor order.
+The GGUF container is left out: the library takes each tensor's block bytes as they sit in
+the file. Also an f64 forward of the same model (model.rs:297-352 with dequantised
+weights and exact arithmetic) to check the GPU layers against."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+from layers import Config, Matrix, inv_freq
+
+M64 = (1 << 64) - 1
+
+
+def tiny_model(n_layer: int, neox: bool):
+    """fixtures.rs:7-60: (Config, layer dicts for GpuLayers, head, embedding Matrix)."""
+    d, ff, vocab, heads, kv_heads = 64, 128, 96, 4, 2
+    state = [0x9E3779B97F4A7C15]
+
+    def rnd(n: int, scale: float) -> np.ndarray:
+        s = state[0]
+        out = np.empty(n, np.float32)
+        for i in range(n):
+            s ^= (s << 13) & M64
+            s ^= s >> 7
+            s ^= (s << 17) & M64
+            out[i] = (np.float32(s % 2001) / np.float32(1000.0) - np.float32(1.0)) * np.float32(scale)
+        state[0] = s
+        return out
+
+    def q8(v: np.ndarray, rows: int, cols: int) -> Matrix:
+        return Matrix(O.Q8_0, O.quantize_q8_0(v).tobytes(), rows, cols)
+
+    embd = q8(rnd(d * vocab, 1.0), vocab, d)
+    kvd = d // heads * kv_heads
+    layers = []
+    for _ in range(n_layer):
+        l = {}
+        l["attn_norm"] = (rnd(d, 0.2) + np.float32(1.0)).astype(np.float32)
+        l["wq"] = q8(rnd(d * d, 0.15), d, d)
+        l["wk"] = q8(rnd(d * kvd, 0.15), kvd, d)
+        l["wv"] = q8(rnd(d * kvd, 0.15), kvd, d)
+        l["bq"] = rnd(d, 0.1)
+        l["bk"] = l["bv"] = None
+        l["wo"] = q8(rnd(d * d, 0.15), d, d)
+        l["ffn_norm"] = (rnd(d, 0.2) + np.float32(1.0)).astype(np.float32)
+        l["gate"] = q8(rnd(d * ff, 0.15), ff, d)
+        l["up"] = q8(rnd(d * ff, 0.15), ff, d)
+        l["down"] = q8(rnd(ff * d, 0.15), d, ff)
+        layers.append(l)
+    head = (np.ones(d, np.float32), q8(rnd(d * vocab, 0.3), vocab, d))
+    cfg = Config(n_embd=d, n_layer=n_layer, n_head=heads, n_head_kv=kv_heads, head_dim=d // heads,
+                 rope_dim=d // heads, rope_base=10000.0, rope_neox=neox, eps=1e-5, vocab=vocab, context=2048)
+    return cfg, layers, head, embd
+
+
+def embed(embd: Matrix, tokens) -> np.ndarray:
+    """Part::embed (model.rs:270-281): the tokens' rows of token_embd, dequantised."""
+    table = O.dequant(embd.type, np.frombuffer(embd.data, np.uint8), embd.rows, embd.cols)
+    return table[np.asarray(tokens, np.int64)].astype(np.float32)
+
+
+class RefModel:
+    """The same layers in f64 over dequantised weights: the reference's CPU forward
+    (model.rs:297-352) with exact arithmetic, its cache a list of rows per layer."""
+
+    def __init__(self, cfg: Config, layers, head):
+        self.cfg = cfg
+        deq = lambda m: O.dequant(m.type, np.frombuffer(m.data, np.uint8), m.rows, m.cols).astype(np.float64)
+        self.layers = []
+        for l in layers:
+            w = {k: deq(l[k]) for k in ("wq", "wk", "wv", "wo", "gate", "up", "down")}
+            for k in ("attn_norm", "ffn_norm"):
+                w[k] = np.asarray(l[k], np.float64)
+            w["bq"] = None if l["bq"] is None else np.asarray(l["bq"], np.float64)
+            self.layers.append(w)
+        self.norm, self.out = np.asarray(head[0], np.float64), deq(head[1])
+        self.freq = inv_freq(cfg).astype(np.float64)
+
+    def new_cache(self):
+        return {"k": [np.zeros((0, self.cfg.n_head_kv * self.cfg.head_dim)) for _ in self.layers],
+                "v": [np.zeros((0, self.cfg.n_head_kv * self.cfg.head_dim)) for _ in self.layers]}
+
+    def _norm(self, x, w):
+        return x / np.sqrt((x * x).mean(axis=1, keepdims=True) + self.cfg.eps) * w
+
+    def _rope(self, t, heads, positions):
+        c = self.cfg
+        t = t.reshape(len(positions), heads, c.head_dim).copy()
+        half = c.rope_dim // 2
+        th = np.asarray(positions, np.float64)[:, None] * self.freq[None, :half]
+        cos, sin = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+        if c.rope_neox:
+            a, b = t[:, :, :half].copy(), t[:, :, half:2 * half].copy()
+            t[:, :, :half], t[:, :, half:2 * half] = a * cos - b * sin, a * sin + b * cos
+        else:
+            a, b = t[:, :, 0:2 * half:2].copy(), t[:, :, 1:2 * half:2].copy()
+            t[:, :, 0:2 * half:2], t[:, :, 1:2 * half:2] = a * cos - b * sin, a * sin + b * cos
+        return t.reshape(len(positions), heads * c.head_dim)
+
+    def forward(self, x, pos: int, tree, cache) -> np.ndarray:
+        c = self.cfg
+        rows = len(x)
+        positions, visible, base = O.shape(rows, pos, tree)
+        x = np.asarray(x, np.float64).copy()
+        hd, nh, nkv = c.head_dim, c.n_head, c.n_head_kv
+        g = nh // nkv
+        for li, w in enumerate(self.layers):
+            n = self._norm(x, w["attn_norm"])
+            q, k, v = n @ w["wq"].T, n @ w["wk"].T, n @ w["wv"].T
+            if w["bq"] is not None:
+                q = q + w["bq"]
+            q, k = self._rope(q, nh, positions), self._rope(k, nkv, positions)
+            kc = np.concatenate([cache["k"][li][:pos], k])
+            vc = np.concatenate([cache["v"][li][:pos], v])
+            cache["k"][li], cache["v"][li] = kc, vc
+            att = np.zeros((rows, nh * hd))
+            for r in range(rows):
+                if visible is None:
+                    slots = np.arange(pos + r + 1)
+                else:
+                    bits = [j for j in range(64) if (int(visible[r]) >> j) & 1]
+                    slots = np.concatenate([np.arange(base), base + np.asarray(bits, np.int64)]).astype(np.int64)
+                for h in range(nh):
+                    kv = h // g
+                    qs = q[r, h * hd:(h + 1) * hd]
+                    s = kc[slots, kv * hd:(kv + 1) * hd] @ qs / np.sqrt(hd)
+                    p = np.exp(s - s.max())
+                    att[r, h * hd:(h + 1) * hd] = (p / p.sum()) @ vc[slots, kv * hd:(kv + 1) * hd]
+            x = x + att @ w["wo"].T
+            n = self._norm(x, w["ffn_norm"])
+            gt, up = n @ w["gate"].T, n @ w["up"].T
+            x = x + (gt / (1.0 + np.exp(-gt)) * up) @ w["down"].T
+        return x
+
+    def logits(self, x) -> np.ndarray:
+        return self._norm(np.asarray(x, np.float64), self.norm) @ self.out.T
