@@ -6,10 +6,11 @@ whole does, a tree pass scores every path as if fed alone (also grown a level at
 Cache::keep keeps the accepted path, and a long conversation grows the cache.
 
 Where the reference holds a one-token pass within 1e-4 of the same row in a batch, these
-tests hold it within 1e-3 x (1 + the largest score): the multi-row attention computes on
-f16 operands (the tolerance the attention path is specified to, max abs 5e-3), the
-one-row kernel on the cache's f32 values. Observed: up to 2.1e-4 on scores up to 5, and
-up to 1.2e-3 against the exact forward."""
+tests hold it within 1e-3 x (1 + the largest score): both attention kernels round q, K, V
+and P to f16 MFMA operands (the attention path's specified tolerance is max abs 5e-3),
+and the one-row kernel takes blocks of 32 entries and a two-level fold where a batch row
+takes blocks of 64 and one left fold, so their roundings differ. Observed: up to 2.1e-4
+on scores up to 5, and up to 1.2e-3 against the exact forward."""
 import numpy as np
 import pytest
 
