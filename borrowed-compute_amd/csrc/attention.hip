@@ -1142,12 +1142,14 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
 // bits of the unsplit one. One thread per (group, slot, 4 dims), in workgroups of one
 // wave so that the few thousand threads spread over as many CUs as they fill (verify: 256
 // workgroups of 64 threads ran the call 1 µs faster than 64 of 256); each pass issues the
-// loads of CMB_RUN chunk states before the first fold step uses them.
-constexpr int CMB_RUN = 32;  // chunk states a thread loads before folding them (one batch up to 8192 entries)
+// loads of RUN chunk states before the first fold step uses them. RUN is the smallest of
+// 8, 16, 24, 32 that holds a shared call's chunks (fewer loads of clamped duplicates: 0.45
+// us off the 70B verify call at 4096 slots), else 32 (one batch up to 8192 entries).
+constexpr int CMB_RUN = 32;
 
 constexpr int CMB_THREADS = 64;
 
-template <int HD>
+template <int HD, int RUN>
 __global__ __launch_bounds__(CMB_THREADS) void attn_combine(const CombineParams p) {
     const uint32_t nd4 = p.hd / 4;
     const uint32_t t = blockIdx.x * CMB_THREADS + threadIdx.x;
@@ -1177,18 +1179,18 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine(const CombineParams 
     const size_t stride = p.slots;  // partial slots per unit
     float M = -INFINITY, L = 0.0f;
     float4 O = float4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t cb = 0; cb < nchunk; cb += CMB_RUN) {
-        float2 ml[CMB_RUN];
-        float4 o[CMB_RUN];
+    for (uint32_t cb = 0; cb < nchunk; cb += RUN) {
+        float2 ml[RUN];
+        float4 o[RUN];
 #pragma unroll
-        for (int j = 0; j < CMB_RUN; j++) {
+        for (int j = 0; j < RUN; j++) {
             const uint32_t c = min(cb + j, nchunk - 1);
             const size_t at = ((size_t)unit0 + (size_t)c * step) * stride + slot;
             ml[j] = *(const float2*)(p.part_ml + at * 2);
             o[j] = *(const float4*)(p.part_o + at * HD + 4 * d4);
         }
 #pragma unroll
-        for (int j = 0; j < CMB_RUN; j++) {
+        for (int j = 0; j < RUN; j++) {
             if (cb + j < nchunk) {
                 float a, b, mn;
                 merge_coef(M, ml[j].x, a, b, mn);
@@ -1552,7 +1554,16 @@ template <int HD>
 static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s) {
     cp.ngroups = groups;
     const uint64_t threads = (uint64_t)groups * cp.slots_out * (cp.hd / 4);
-    hipLaunchKernelGGL((attn_combine<HD>), dim3(ceil_div(threads, CMB_THREADS)), dim3(CMB_THREADS), 0, s, cp);
+    const dim3 grid(ceil_div(threads, CMB_THREADS)), block(CMB_THREADS);
+    const uint32_t nc = cp.shared ? cp.nchunk : (uint32_t)CMB_RUN;
+    if (nc <= 8)
+        hipLaunchKernelGGL((attn_combine<HD, 8>), grid, block, 0, s, cp);
+    else if (nc <= 16)
+        hipLaunchKernelGGL((attn_combine<HD, 16>), grid, block, 0, s, cp);
+    else if (nc <= 24)
+        hipLaunchKernelGGL((attn_combine<HD, 24>), grid, block, 0, s, cp);
+    else
+        hipLaunchKernelGGL((attn_combine<HD, CMB_RUN>), grid, block, 0, s, cp);
     return hipGetLastError();
 }
 
