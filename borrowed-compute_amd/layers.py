@@ -11,6 +11,8 @@ growth, mod.rs:404-423); positions and the tree's visibility masks come from the
 Shape (model.rs:405-443), as in the reference."""
 from __future__ import annotations
 
+import ctypes
+import ctypes.util
 import math
 from dataclasses import dataclass
 
@@ -35,14 +37,30 @@ class Config:
     context: int = 4096
 
 
+_libm = None
+
+
+def _powf(x: float, y: float) -> float:
+    """The C library's single-precision pow, the one the reference's f32::powf calls
+    (numpy's float32 power differs from it in the last bit for many of these arguments)."""
+    global _libm
+    if _libm is None:
+        _libm = ctypes.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+        _libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+        _libm.powf.restype = ctypes.c_float
+    return _libm.powf(x, y)
+
+
 def inv_freq(cfg: Config, factors=None) -> np.ndarray:
-    """model.rs:208-211: rope_base^(-2i / rope_dim) in f32, over the optional per-pair
-    factors (rope_freqs.weight)."""
-    i = np.arange(cfg.rope_dim // 2, dtype=np.float32)
-    e = (np.float32(-2.0) * i) / np.float32(cfg.rope_dim)
-    f = np.power(np.float32(cfg.rope_base), e, dtype=np.float32)
+    """model.rs:208-211: rope_base^(-2i / rope_dim) in f32 (the exponent rounded to f32
+    first), over the optional per-pair factors (rope_freqs.weight)."""
+    half = cfg.rope_dim // 2
+    f = np.empty(half, np.float32)
+    for i in range(half):
+        e = np.float32(np.float32(-2.0) * np.float32(i)) / np.float32(cfg.rope_dim)
+        f[i] = _powf(np.float32(cfg.rope_base), e)
     if factors is not None:
-        f = (f / np.asarray(factors, np.float32)[: len(f)]).astype(np.float32)
+        f = (f / np.asarray(factors, np.float32)[:half]).astype(np.float32)
     return f
 
 

@@ -71,3 +71,16 @@ def test_cache_capacity_grows_as_the_reference_reserve():
     for cap, need, context in [(0, 1, 8), (256, 900, 100000), (1 << 20, (1 << 20) + 1, 1 << 22)]:
         got = grown_capacity(cap, need, context)
         assert got >= need and (got >= min(2 * cap, context) or got == need)
+
+
+def test_stage_rope_frequencies_are_the_reference_f32_values():
+    """layers.inv_freq (the host side of a stage) against the oracle's restatement of
+    model.rs:208-211 (f32 powf), bit for bit, over the bases and widths the configs use."""
+    import numpy as np
+    import oracle as O
+    from layers import Config, inv_freq
+    for base in (10000.0, 500000.0, 1000000.0, 37000.0):
+        for rd in (16, 32, 64, 96, 128, 256):
+            got = inv_freq(Config(64, 1, 4, 2, rd, rd, base))
+            np.testing.assert_array_equal(got.view(np.uint32), O.inv_freq(rd, base).view(np.uint32),
+                                          err_msg=f"base {base}, rope_dim {rd}")
