@@ -55,17 +55,6 @@ __device__ __forceinline__ void state_clear(State<NDT>& s) {
     s.l = 0.0f;
 }
 
-__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Coefficients of merging a state with max M and one with max m: new max Mn, weights a
-// (for the first) and b (for the second). An empty state (max -inf) gets weight 0, and
-// merging into an empty state leaves the other exactly as it was.
-__device__ __forceinline__ void merge_coef(float M, float m, float& a, float& b, float& Mn) {
-    Mn = fmaxf(M, m);
-    float ms = (Mn == -INFINITY) ? 0.0f : Mn;
-    a = exp2_hw(M - ms);
-    b = exp2_hw(m - ms);
-}
 
 // The running max of a slot moves only when a block's max passes it by more than LAZY
 // (log2 units): until then the block's P = 2^(x - m) may reach 2^LAZY (exact in f16's
@@ -301,15 +290,6 @@ __device__ __forceinline__ half8 q_operand(const float* __restrict__ qrow, uint3
 template <int VS>
 __device__ __forceinline__ void v_store(f16* __restrict__ vl, int kl, uint32_t d0, half8 v) {
     *(half8*)&vl[kl * VS + d0] = v;
-}
-
-// Position of the k-th set bit of (lo, hi), k < popcount.
-__device__ __forceinline__ uint32_t nth_set_bit(uint32_t lo, uint32_t hi, uint32_t k) {
-    uint32_t cl = __popc(lo);
-    uint32_t w = k < cl ? lo : hi, off = k < cl ? 0u : 32u;
-    k = k < cl ? k : k - cl;
-    for (uint32_t i = 0; i < k; i++) w &= w - 1u;  // drop the k lowest set bits
-    return off + (uint32_t)__builtin_ctz(w);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1591,6 +1571,12 @@ static int pad_hd(uint32_t hd) {
 template <int HD>
 static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s);
 
+hipError_t combine_launch(CombineParams& cp, uint32_t groups, uint32_t hd, hipStream_t s) {
+    hipError_t e;
+    BCHIP_DISPATCH_HD(pad_hd(hd), e = (launch_combine_t<HD>(cp, groups, s)));
+    return e;
+}
+
 template <int HD, typename KVT>
 static hipError_t launch_decode_t(DirectParams& dp, CombineParams& cp, const AttnCall& a, hipStream_t s) {
     // Tree rows only: lines of any length go to the shared kernels, one-row lists to the
@@ -1651,6 +1637,11 @@ uint32_t row_chunk(uint64_t len, uint32_t nkv) {
     uint64_t chunk = (len + most - 1) / most;
     chunk = (chunk + RB - 1) / RB * RB;
     return (uint32_t)std::max<uint64_t>(chunk, 2 * RB);
+}
+
+size_t row_state_slots(uint64_t len, uint32_t nkv) {
+    const uint64_t chunk = row_chunk(len, nkv);
+    return (size_t)nkv * ((len + chunk - 1) / chunk) * 16;
 }
 
 bool row_fusable(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox) {
@@ -1714,11 +1705,9 @@ static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nite
     dp.part_o = ws.o;
     dp.part_ml = ws.ml;
     dp.qrot = ws.qrot;
-    if (a.kv_type == 1) {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, f16>(dp, fold, a, s)));
-    } else {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, float>(dp, fold, a, s)));
-    }
+    // f16 caches only: f32 caches take the f32 path (attention_f32.hip).
+    if (a.kv_type != 1) return hipErrorInvalidValue;
+    BCHIP_DISPATCH_HD(hdp, e = (launch_row_t<HD, f16>(dp, fold, a, s)));
     return e;
 }
 
@@ -1755,11 +1744,8 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
     cp.shared = 0;
     cp.nitems = nitems;
     for (uint32_t i = 0; i < nitems; i++) cp.items[i] = dp.items[i];
-    if (a.kv_type == 1) {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, f16>(dp, cp, a, s)));
-    } else {
-        BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, float>(dp, cp, a, s)));
-    }
+    if (a.kv_type != 1) return hipErrorInvalidValue;
+    BCHIP_DISPATCH_HD(hdp, e = (launch_decode_t<HD, f16>(dp, cp, a, s)));
     return e;
 }
 
@@ -1817,20 +1803,14 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
             hipExtLaunchKernelGGL((attn_prefill<4, false>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
         }
         e = hipGetLastError();
-    } else {
-        if (a.kv_type == 1) {
-            if (wide) {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, a, s)));
-            } else {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, 1>(sp, blocks, a, s)));
-            }
+    } else if (a.kv_type == 1) {
+        if (wide) {
+            BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, a, s)));
         } else {
-            if (wide) {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, (HD <= 128 ? 2 : 1)>(sp, blocks, a, s)));
-            } else {
-                BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, float, 4, 1>(sp, blocks, a, s)));
-            }
+            BCHIP_DISPATCH_HD(hdp, e = (launch_shared_t<HD, f16, 4, 1>(sp, blocks, a, s)));
         }
+    } else {
+        return hipErrorInvalidValue;  // f32 caches take the f32 path (attention_f32.hip)
     }
     if (e != hipSuccess || !sp.split) return e;
     CombineParams cp{};

@@ -121,7 +121,25 @@ int check_heads(uint32_t nh, uint32_t nkv, uint32_t hd) {
 
 namespace bchip {
 
+void Workspace::set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_bytes, void* zero_page) {
+    fixed = true;
+    o = (float*)base;
+    ml = (float*)((char*)base + o_bytes);
+    qrot = (float*)((char*)base + o_bytes + ml_bytes);
+    o_cap = o_bytes;
+    ml_cap = ml_bytes;
+    qrot_cap = q_bytes;
+    zero = zero_page;
+}
+
 hipError_t Workspace::reserve(size_t need_slots, size_t hd_pad) {
+    if (fixed) {
+        if (need_slots * hd_pad * sizeof(float) > o_cap || need_slots * 2 * sizeof(float) > ml_cap)
+            return hipErrorOutOfMemory;
+        slots = need_slots;
+        hdp = hd_pad;
+        return hipSuccess;
+    }
     if (need_slots <= slots && hd_pad <= hdp && o) return hipSuccess;
     const size_t ns = std::max(need_slots, slots), nh = std::max(hd_pad, hdp);
     if (o) (void)hipFree(o);
@@ -138,6 +156,7 @@ hipError_t Workspace::reserve(size_t need_slots, size_t hd_pad) {
 }
 
 hipError_t Workspace::reserve_vt(size_t bytes) {
+    if (fixed) return hipErrorOutOfMemory;
     if (bytes <= vt_bytes && vt) return hipSuccess;
     if (vt) (void)hipFree(vt);
     vt = nullptr;
@@ -149,6 +168,11 @@ hipError_t Workspace::reserve_vt(size_t bytes) {
 }
 
 hipError_t Workspace::reserve_qrot(size_t floats) {
+    if (fixed) {
+        if (floats * sizeof(float) > qrot_cap) return hipErrorOutOfMemory;
+        qrot_floats = floats;
+        return hipSuccess;
+    }
     if (floats <= qrot_floats && qrot) return hipSuccess;
     if (qrot) (void)hipFree(qrot);
     qrot = nullptr;
@@ -166,6 +190,7 @@ hipError_t Workspace::init() {
 }
 
 void Workspace::release() {
+    if (fixed) return;  // a view of memory this workspace does not own
     if (o) (void)hipFree(o);
     if (ml) (void)hipFree(ml);
     if (vt) (void)hipFree(vt);
@@ -467,6 +492,7 @@ int bchip_rope_append(bchip_ctx* c, float* q, const float* k, const float* v, vo
     CHECK(check_span(c, kc, (slot0 + rows) * kvd * esize(kv_type), "kc"));
     CHECK(check_span(c, vc, (slot0 + rows) * kvd * esize(kv_type), "vc"));
     CHECK(check_span(c, positions, (uint64_t)rows * 4, "positions"));
+    CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
     HIP_TRY(rope_append_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, rows, nh, nkv, hd, rope_dim, neox,
                                slot0, c->stream),
             "rope_append");
@@ -487,6 +513,7 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     if (tree) {
         if (!masks) return fail(BCHIP_E_ARG, "a tree needs its masks");
         if (rows > MAX_ITEMS) return fail(BCHIP_E_ARG, "a tree pass of %u rows (at most %u)", rows, MAX_ITEMS);
+        if ((uint64_t)pos + MAX_ITEMS > 0xffffffffull) return fail(BCHIP_E_ARG, "tree slots past 2^32");
         CHECK(check_span(c, masks, (uint64_t)rows * 8, "masks"));
     }
     const uint64_t kvd = (uint64_t)nkv * hd, slots = (uint64_t)pos + rows;
@@ -499,26 +526,35 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     AttnCall a{q, kc, vc, kv_type, out, masks, tree ? 1u : 0u, rows, nh, nkv, hd, pos, scale, limit};
     c->take_marks(a);
     hipError_t e;
-    // One row: the one-row kernel. Tree rows: each row gathers its own list (decode-kernel
-    // units). Lines of two or more rows (prefill, speculative verify): the shared kernels,
-    // which read each K/V block once for every row and head of a KV head they hold (split
-    // over the list when there are few of them). Every multi-row kernel computes a row with
-    // the same arithmetic, so the choice does not change a bit of the result.
-    if (rows == 1 && !tree) {
+    // f32 caches: the f32 path, one arithmetic for every row of every pass.
+    // f16 caches: one row: the one-row kernel. Tree rows: each row gathers its own list
+    // (decode-kernel units). Lines of two or more rows (prefill, speculative verify): the
+    // shared kernels, which read each K/V block once for every row and head of a KV head they
+    // hold (split over the list when there are few of them). Every multi-row kernel computes a
+    // row with the same arithmetic, so the choice does not change a bit of the result.
+    if (kv_type == BCHIP_F32) {
+        e = f32_attention(a, 0, c->ws, c->stream);
+    } else if (rows == 1 && !tree) {
         Item item{};
         item.row = 0;
         item.nrows = 1;
         item.len = (uint32_t)slots;
         e = row_attention(a, &item, 1, c->ws, c->stream);
     } else if (tree) {
+        // A row's list is pos + popcount(its mask), and a tree grown a level at a time holds
+        // more nodes than the pass has rows (Shape::new, model.rs:421-443): a row's mask may
+        // name any of slots pos .. pos + 63. The chunks cover that farthest list; a chunk
+        // past a row's own list computes nothing and leaves an empty state, which the fold
+        // takes as the identity (weight 0, the running state's weight exactly 1).
+        const uint64_t far = (uint64_t)pos + MAX_ITEMS;
         Item items[MAX_ITEMS];
         for (uint32_t i = 0; i < rows; i++) {
             Item& I = items[i];
             I = Item{};
             I.row = i;
             I.nrows = 1;
-            I.len = (uint32_t)slots;
-            I.nchunk = (uint32_t)((slots + CHUNK_MULTI - 1) / CHUNK_MULTI);
+            I.len = (uint32_t)std::min<uint64_t>(far, 0xffffffffull);
+            I.nchunk = (uint32_t)((far + CHUNK_MULTI - 1) / CHUNK_MULTI);
             I.chunk = CHUNK_MULTI;
         }
         e = direct_attention(a, items, rows, c->ws, c->stream);
@@ -529,20 +565,19 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     return BCHIP_OK;
 }
 
-int bchip_rope_append_attention(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc,
-                                uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,
-                                uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos,
-                                float scale, float* out) {
+// bchip_rope_append_attention on workspace ws; with a fixed workspace (the no-allocation
+// entry point) every launch's scratch is checked to fit before anything is launched.
+static int fused_step(bchip_ctx* c, Workspace& ws, float* q, const float* k, const float* v, void* kc, void* vc,
+                      uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,
+                      uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos, float scale,
+                      float* out) {
     CHECK(enter(c));
     if (!q || !k || !v || !kc || !vc || !inv_freq || !positions || !out) return fail(BCHIP_E_ARG, "null pointer");
     if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
     CHECK(check_heads(nh, nkv, hd));
     if (rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
-    if (!row_fusable(nh, nkv, hd, rope_dim, neox)) {
-        CHECK(bchip_rope_append(c, q, k, v, kc, vc, kv_type, inv_freq, positions, 1, nh, nkv, hd, rope_dim, neox, pos));
-        return bchip_attention(c, q, kc, vc, kv_type, out, nullptr, 0, 1, nh, nkv, hd, pos, scale);
-    }
-    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc) || !aligned16(k) || !aligned16(v))
+    const bool fuse = kv_type == BCHIP_F16 && row_fusable(nh, nkv, hd, rope_dim, neox);
+    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc) || (fuse && (!aligned16(k) || !aligned16(v))))
         return fail(BCHIP_E_ARG, "q, k, v, out and the caches must be 16-byte aligned");
     if ((uint64_t)pos + 1 > 0xffffffffull) return fail(BCHIP_E_ARG, "position past 2^32");
     const uint64_t kvd = (uint64_t)nkv * hd, slots = (uint64_t)pos + 1;
@@ -554,12 +589,46 @@ int bchip_rope_append_attention(bchip_ctx* c, float* q, const float* k, const fl
     CHECK(check_span(c, vc, slots * kvd * esize(kv_type), "vc"));
     CHECK(check_span(c, positions, 4, "positions"));
     CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
+    if (ws.fixed && kv_type == BCHIP_F16) {
+        const size_t hdp = hd <= 32 ? 32 : hd <= 64 ? 64 : hd <= 128 ? 128 : 256;
+        const size_t need = row_state_slots(slots, nkv);
+        if (need * hdp * 4 > ws.o_cap || need * 8 > ws.ml_cap || (fuse && (size_t)nh * hd * 4 > ws.qrot_cap))
+            return fail(BCHIP_E_ARG,
+                        "this step takes %zu bytes of chunk states and %zu of staged q; the no-allocation "
+                        "entry point holds %zu and %zu",
+                        need * hdp * 4, fuse ? (size_t)nh * hd * 4 : (size_t)0, ws.o_cap, ws.qrot_cap);
+    }
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
     AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, pos, scale, limit};
     c->take_marks(a);
+    if (!fuse) {
+        // f32 caches, and shapes the fused kernel does not take: the two calls.
+        HIP_TRY(rope_append_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, 1, nh, nkv, hd, rope_dim, neox,
+                                   pos, c->stream),
+                "rope_append");
+        if (kv_type == BCHIP_F32) {
+            HIP_TRY(f32_attention(a, 0, ws, c->stream), "attention");
+        } else {
+            Item item{};
+            item.row = 0;
+            item.nrows = 1;
+            item.len = (uint32_t)slots;
+            HIP_TRY(row_attention(a, &item, 1, ws, c->stream), "attention");
+        }
+        return BCHIP_OK;
+    }
     RopeArgs r{q, k, v, inv_freq, positions, rope_dim, neox};
-    HIP_TRY(row_attention_fused(a, r, c->ws, c->stream), "rope_append_attention");
+    HIP_TRY(row_attention_fused(a, r, ws, c->stream), "rope_append_attention");
     return BCHIP_OK;
+}
+
+int bchip_rope_append_attention(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc,
+                                uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,
+                                uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos,
+                                float scale, float* out) {
+    if (!c) return fail(BCHIP_E_ARG, "no context");
+    return fused_step(c, c->ws, q, k, v, kc, vc, kv_type, inv_freq, positions, nh, nkv, hd, rope_dim, neox, pos,
+                      scale, out);
 }
 
 int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const void* vc, uint32_t kv_type,
@@ -585,6 +654,24 @@ int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const v
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
     AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, 0u, scale, limit};
     c->take_marks(a);
+    if (kv_type == BCHIP_F32) {
+        // One f32-path call per sequence, each at its place in the pool, its result the bits of
+        // the sequence alone. The workspace is sized for the longest first, so that no call
+        // reallocates it while an earlier one may still read it.
+        uint32_t longest = 0;
+        for (uint32_t i = 0; i < nseq; i++) longest = std::max(longest, seq_lens[i]);
+        const size_t most = (size_t)nkv * ((longest + CHUNK_MULTI - 1) / CHUNK_MULTI) * 16;
+        HIP_TRY(c->ws.reserve(most, hd <= 32 ? 32 : hd <= 64 ? 64 : hd <= 128 ? 128 : 256), "workspace");
+        for (uint32_t i = 0; i < nseq; i++) {
+            AttnCall ai = a;
+            ai.q = q + (size_t)i * nh * hd;
+            ai.out = out + (size_t)i * nh * hd;
+            ai.pos = seq_lens[i] - 1;
+            if (i > 0) ai.ev_before = ai.ev_after = nullptr;
+            HIP_TRY(f32_attention(ai, kv_offsets[i], c->ws, c->stream), "ragged attention");
+        }
+        return BCHIP_OK;
+    }
     for (uint32_t s0 = 0; s0 < nseq; s0 += MAX_ITEMS) {
         const uint32_t ns = std::min<uint32_t>(MAX_ITEMS, nseq - s0);
         Item items[MAX_ITEMS];

@@ -34,6 +34,30 @@ __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Coefficients of merging a softmax state with max M (log2 units) and one with max m: new
+// max Mn, weights a (for the first) and b (for the second). An empty state (max -inf) gets
+// weight 0 and the other weight exactly 1 (2^0), so folding an empty state in, or folding
+// into an empty state, leaves the other exactly as it was. Every fold of chunk states (in a
+// kernel or in attn_combine) uses this and the same per-element expression,
+// R = R * a + c * b, so a fold gives the same bits wherever it runs.
+__device__ __forceinline__ void merge_coef(float M, float m, float& a, float& b, float& Mn) {
+    Mn = fmaxf(M, m);
+    float ms = (Mn == -INFINITY) ? 0.0f : Mn;
+    a = exp2_hw(M - ms);
+    b = exp2_hw(m - ms);
+}
+
+// Position of the k-th set bit of (lo, hi), k < popcount.
+__device__ __forceinline__ uint32_t nth_set_bit(uint32_t lo, uint32_t hi, uint32_t k) {
+    uint32_t cl = __popc(lo);
+    uint32_t w = k < cl ? lo : hi, off = k < cl ? 0u : 32u;
+    k = k < cl ? k : k - cl;
+    for (uint32_t i = 0; i < k; i++) w &= w - 1u;  // drop the k lowest set bits
+    return off + (uint32_t)__builtin_ctz(w);
+}
+
 // The rotation of one RoPE pair by theta: y0 = x0 cos - x1 sin, y1 = x0 sin + x1 cos, each
 // product rounded on its own (model.rs:395-400), sincosf the device library's full-range
 // one. Every kernel that rotates uses this, so a row rotated anywhere has the same bits.

@@ -9,7 +9,9 @@
 
 namespace bchip {
 
-// Device scratch for split-K partials, owned by a context and grown on demand.
+// Device scratch for split-K partials, owned by a context and grown on demand; or, fixed,
+// a view of memory set aside once (the no-allocation entry point's): then a reserve beyond
+// it fails with hipErrorOutOfMemory and nothing is allocated.
 struct Workspace {
     float* o = nullptr;    // [units*slots][hd_pad]: chunk states
     float* ml = nullptr;   // [units*slots][2]
@@ -17,7 +19,12 @@ struct Workspace {
     void* vt = nullptr;    // V^T tiles of a prefill call
     float* qrot = nullptr;  // rotated q of a fused step, until attn_row_fold copies it
     size_t slots = 0, hdp = 0, vt_bytes = 0, qrot_floats = 0;
+    bool fixed = false;
+    size_t o_cap = 0, ml_cap = 0, qrot_cap = 0;  // fixed: bytes of o, ml and qrot
     hipError_t init();     // allocates the zero page
+    // The fixed view: o, ml and qrot at base (o_bytes, ml_bytes, q_bytes each), the zero page
+    // of `zero_page`.
+    void set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_bytes, void* zero_page);
     hipError_t reserve(size_t need_slots, size_t hd_pad);
     hipError_t reserve_qrot(size_t floats);
     hipError_t reserve_vt(size_t bytes);
@@ -57,10 +64,17 @@ struct RopeArgs {
 };
 hipError_t row_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s);
 bool row_fusable(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox);
+// Workspace slots (chunk states) a one-row call over a list of len entries takes.
+size_t row_state_slots(uint64_t len, uint32_t nkv);
 // Tree rows as items with chunk and nchunk set (CHUNK_MULTI).
 hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
                             Workspace& ws, hipStream_t s);
 hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s);
+// The left fold of chunk states (attn_combine) over `groups` groups of cp.
+hipError_t combine_launch(CombineParams& cp, uint32_t groups, uint32_t hd, hipStream_t s);
+// Every call on an f32 cache (lines, trees, one row): f32 arithmetic throughout
+// (attention_f32.hip). kvoff: slot offset of the row's cache in a ragged pool.
+hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipStream_t s);
 
 hipError_t rope_launch(float* x, const float* inv_freq, const uint32_t* positions, uint32_t rows,
                        uint32_t heads, uint32_t hd, uint32_t rope_dim, uint32_t neox, hipStream_t s);

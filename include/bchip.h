@@ -125,7 +125,16 @@ int bchip_rope_append(bchip_ctx* ctx, float* q, const float* k, const float* v, 
  *    masks[2r+1] (bits 32-63) (device u32 [2*rows], mod.rs:436-442), summed in list order:
  *    the k-th entry of the list is slot k below pos, then the (k-pos)-th set bit
  *    (kernels.h:266-278), so a tree row gets exactly the bits of the line its path is.
+ *     A tree grown a level at a time holds more nodes than the pass has rows (Shape::new,
+ *    model.rs:421-443), so a mask may name any slot up to pos + 63: the caches must hold
+ *    every slot the masks name (the caller's Shape guarantees it; in a bchip_alloc buffer a
+ *    slot past its end reads as zeros, never out of bounds). rows <= 64, pos + 64 <= 2^32.
  * Requires hd % 8 == 0, hd <= 256, nh % nkv == 0, nh/nkv <= 16.
+ * f32 caches (the reference's): f32 arithmetic throughout, the scores by quant::dot's
+ * eight-lane sum (quant.rs:617-631), one arithmetic for every row of every call: a row's
+ * bits depend only on its q and its visible slot list, whatever the batch, the row's index,
+ * tree or line, one row or many (model.rs:531, 578, 592-594, 641-646).
+ * f16 caches: q, K, V and the softmax weights are f16 MFMA operands, f32 accumulation.
  * Every row of a multi-row call (rows >= 2) is computed by the same fixed-order
  * arithmetic, which depends only on the row's q and its visible slot list: results are
  * identical whatever the batch, the row's index, or whether it is a tree node or a line
@@ -144,8 +153,9 @@ int bchip_attention(bchip_ctx* ctx, const float* q, const void* kc, const void* 
  * five commands k_rope(q), k_rope(k), k_copy(k), k_copy(v), k_attention that
  * Layers::forward queues per layer for a one-token pass (gpu/mod.rs:464-482): the rotation
  * and the append run inside the attention kernel, which takes the new row from registers.
- * Shapes the fused kernel does not take (hd % 32 != 0, or neox pairs with rope_dim/2 not a
- * multiple of 32) run as the two calls. positions: device u32 [1]. */
+ * f32 caches, and shapes the fused kernel does not take (hd % 32 != 0, neox pairs with
+ * rope_dim/2 not a multiple of 32, or more than 8 query heads per KV head), run as the two
+ * calls. positions: device u32 [1]. */
 int bchip_rope_append_attention(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
                                 uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,
                                 uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos,

@@ -147,6 +147,9 @@ PREFILL = [
     (3, 2000, 28, 4, 128, bchip.F16),   # short line over 8 chunks, G = 7
     (2, 190, 32, 8, 128, bchip.F16),    # lists of 191 and 192: the second ends a chunk
     (4, 381, 28, 4, 128, bchip.F16),    # lists 382..385 across the second chunk's end
+    (300, 0, 28, 4, 128, bchip.F16),    # packed-V^T prefill with G = 7 (workgroups straddle heads)
+    (2, 190, 32, 8, 128, bchip.F32),    # f32 path: lists of 191 and 192
+    (40, 370, 8, 2, 64, bchip.F32),     # f32 path: a row block across the second chunk's end
 ]
 
 
@@ -321,6 +324,56 @@ def test_tree_grown_a_level_at_a_time(ctx):
     a.free()
 
 
+@pytest.mark.parametrize("prefix,kv_type", [(190, bchip.F16), (191, bchip.F16), (190, bchip.F32)])
+def test_grown_tree_level_whose_list_passes_its_rows(ctx, prefix, kv_type):
+    """A tree fed a level at a time (model.rs:580-594): the last level of [ROOT, ROOT, 0, 0,
+    2] is one row that sees the prefix and nodes 0, 2 and 4, so its list (prefix + 3) runs
+    past prefix + rows, across the first 192-entry chunk's end. Against the oracle, and bit
+    for bit against the line its path is."""
+    nh, nkv, hd = 8, 2, 64
+    parents = [O.ROOT, O.ROOT, 0, 0, 2]
+    n = prefix + len(parents)
+    q = rand((len(parents), nh, hd), prefix)
+    kc, vc = rand((n, nkv * hd), prefix + 1), rand((n, nkv * hd), prefix + 2)
+    a = Attn(ctx, kc, vc, kv_type, nh, nkv, hd)
+    _, vis, base = O.shape(1, prefix + 4, parents)
+    assert base == prefix and int(vis[0]) == 0b10101
+    got = a.run(q[4:5], 1, base, 0.125, vis)
+    a.free()
+    check_against_oracle(got, q[4:5], kc, vc, kv_type, 1, prefix + 4, nh, nkv, hd, 0.125, vis, base, "grown level")
+    path = [0, 2, 4]
+    lk = np.concatenate([kc[:prefix], kc[[prefix + j for j in path]]])
+    lv = np.concatenate([vc[:prefix], vc[[prefix + j for j in path]]])
+    lq = rand((prefix + 3, nh, hd), 98)
+    lq[-1] = q[4]
+    line = Attn(ctx, lk, lv, kv_type, nh, nkv, hd)
+    want = line.run(lq, prefix + 3, 0, 0.125)
+    line.free()
+    np.testing.assert_array_equal(got[0], want[-1])
+
+
+@pytest.mark.parametrize("kv_type", [bchip.F16, bchip.F32])
+def test_grown_tree_level_across_the_second_chunk(ctx, kv_type):
+    """A chain of 8 nodes after 380 slots, fed as two levels of 4: the second level's rows see
+    lists of 385..388 entries, across the second chunk's end (384), while the pass's rows end
+    at 384. Every row against the oracle and against the same rows of the whole tree in one
+    pass, bit for bit."""
+    nh, nkv, hd, prefix = 4, 2, 16, 380
+    parents = [O.ROOT, 0, 1, 2, 3, 4, 5, 6]
+    n = prefix + 8
+    q = rand((8, nh, hd), 11)
+    kc, vc = rand((n, nkv * hd), 12), rand((n, nkv * hd), 13)
+    a = Attn(ctx, kc, vc, kv_type, nh, nkv, hd)
+    _, vis_all, base = O.shape(8, prefix, parents)
+    whole = a.run(q, 8, base, 0.25, vis_all)
+    _, vis, b2 = O.shape(4, prefix + 4, parents)
+    assert b2 == base
+    part = a.run(q[4:], 4, b2, 0.25, vis)
+    a.free()
+    check_against_oracle(part, q[4:], kc, vc, kv_type, 4, prefix + 4, nh, nkv, hd, 0.25, vis, b2, "second level")
+    np.testing.assert_array_equal(part, whole[4:])
+
+
 def test_ragged_matches_single_sequence_decode(ctx):
     """Config 4's layout: sequences of different lengths in one pool, one launch; each
     sequence's result is its own one-row pass, bit for bit, and matches the oracle."""
@@ -375,5 +428,12 @@ def test_bad_arguments_are_refused_before_launch(ctx):
         ctx.attention(q, kc, kc, bchip.F16, out, None, False, 1, 32, 5, 128, 0, 0.1)
     with pytest.raises(bchip.BchipError):  # a tree without masks
         ctx.attention(q, kc, kc, bchip.F16, out, None, True, 1, 32, 8, 128, 0, 0.1)
-    for b in (kc, q, out):
+    # bchip_rope_append: an inv_freq buffer shorter than rope_dim / 2 floats.
+    inv = ctx.zeros(16 * 4)
+    pos = ctx.zeros(4)
+    kn = ctx.zeros(8 * 128 * 4)
+    with pytest.raises(bchip.BchipError) as e:
+        ctx.rope_append(q, kn, kn, kc, kc, bchip.F16, inv, pos, 1, 32, 8, 128, 128, False, 0)
+    assert "inv_freq" in str(e.value)
+    for b in (kc, q, out, inv, pos, kn):
         b.free()

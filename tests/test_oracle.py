@@ -114,6 +114,26 @@ def test_tree_attention_matches_brute_force_and_sdpa():
     np.testing.assert_allclose(got, ref.permute(1, 0, 2).numpy(), atol=2e-5)
 
 
+@pytest.mark.parametrize("prefix", [190, 191, 380])
+def test_grown_tree_level_sees_nodes_past_its_rows(prefix):
+    """A tree fed a level at a time (model.rs:421-443, 580-594): the last level of
+    [ROOT, ROOT, 0, 0, 2] is one row at position prefix + 4 whose list is the prefix and
+    nodes 0, 2 and 4 (prefix + 3 entries: past prefix + rows). The oracle's row against the
+    f64 brute force and against its path fed as a line."""
+    nh, nkv, hd = 8, 2, 64
+    parents = [O.ROOT, O.ROOT, 0, 0, 2]
+    n = prefix + 5
+    q = rand((1, nh, hd), 71)
+    kc, vc = rand((n, nkv * hd), 72), rand((n, nkv * hd), 73)
+    _, vis, base = O.shape(1, prefix + 4, parents)
+    assert base == prefix and int(vis[0]) == 0b10101
+    got = O.attention(q, kc, vc, 1, prefix + 4, nh, nkv, hd, 0.125, visible=vis, base=base)
+    np.testing.assert_allclose(got, brute(q, kc, vc, 1, prefix + 4, nh, nkv, hd, 0.125, vis, base), atol=2e-5)
+    idx = list(range(prefix)) + [prefix + j for j in (0, 2, 4)]
+    line = O.attention(q, kc[idx], vc[idx], 1, prefix + 2, nh, nkv, hd, 0.125)
+    np.testing.assert_array_equal(got, line)
+
+
 def test_golden_fixtures():
     """Vectors written by tests/golden/make_golden.py from torch SDPA in f64."""
     files = sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz"))
