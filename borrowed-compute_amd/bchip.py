@@ -78,6 +78,8 @@ def lib() -> ctypes.CDLL:
         "bchip_rope_append": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, u64], i32),
         "bchip_attention": ([P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32], i32),
         "bchip_rope_append_attention": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32, P], i32),
+        "bchip_rope_append_attention_noalloc": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32,
+                                                 P], i32),
         "bchip_attention_ragged": ([P, P, P, P, u32, P, P, P, u32, u32, u32, u32, f32], i32),
         "bchip_fill_normal": ([P, P, u32, u64, u64], i32),
         "bchip_matmul": ([P, P, u32, P, P, u32, u32, u32], i32),
@@ -226,6 +228,13 @@ class Ctx:
         check(lib().bchip_rope_append_attention(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc), kv_type,
                                                 _ptr(inv_freq), _ptr(positions), nh, nkv, hd, rope_dim, int(neox),
                                                 pos, scale, _ptr(out)))
+
+    def rope_append_attention_noalloc(self, q, k, v, kc, vc, kv_type, inv_freq, positions, nh, nkv, hd, rope_dim,
+                                      neox, pos, scale, out) -> None:
+        """bchip_rope_append_attention with the library's fixed scratch: no device allocation."""
+        check(lib().bchip_rope_append_attention_noalloc(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc),
+                                                        kv_type, _ptr(inv_freq), _ptr(positions), nh, nkv, hd,
+                                                        rope_dim, int(neox), pos, scale, _ptr(out)))
 
     def attention_ragged(self, q, kc, vc, kv_type, out, seq_lens, kv_offsets, nh, nkv, hd, scale) -> None:
         lens = np.ascontiguousarray(seq_lens, np.uint32)

@@ -24,11 +24,24 @@
 
 using namespace bchip;
 
+// The scratch of bchip_rope_append_attention_noalloc: a one-row step's chunk states
+// (NOALLOC_O_BYTES: 1024 units x 16 slots x 256 dims, the most a one-row plan takes for
+// nkv <= 1024), their maxima and sums, and a fused step's staged rotated q (nh * hd <= 65536).
+// Each device holds its own copy from the library's load until the process ends; every call
+// on one device shares it, so calls on one device that overlap in time race. Host code never
+// names it: bchip_init takes its device address (hipGetSymbolAddress) and uses that.
+constexpr size_t NOALLOC_O_BYTES = (size_t)16 << 20;
+constexpr size_t NOALLOC_ML_BYTES = (size_t)128 << 10;
+constexpr size_t NOALLOC_Q_BYTES = (size_t)256 << 10;
+constexpr size_t NOALLOC_BYTES = NOALLOC_O_BYTES + NOALLOC_ML_BYTES + NOALLOC_Q_BYTES;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
+
 struct bchip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     Workspace ws;
+    Workspace fixed_ws;  // the scratch array's device copy, for the no-allocation entry point
     std::map<uintptr_t, size_t> allocs;  // base -> bytes, of bchip_alloc memory
     std::string name;
     hipEvent_t arm_before = nullptr, arm_after = nullptr;  // bchip_timer_arm, for the next call
@@ -231,6 +244,12 @@ int bchip_init(int device, bchip_ctx** out) {
               std::to_string(prop.multiProcessorCount) + " CUs)";
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = c->ws.init();
+    if (e == hipSuccess) {
+        // This device's copy of the no-allocation scratch (the device is current here).
+        void* sp = nullptr;
+        e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        if (e == hipSuccess) c->fixed_ws.set_fixed(sp, NOALLOC_O_BYTES, NOALLOC_ML_BYTES, NOALLOC_Q_BYTES, c->ws.zero);
+    }
     if (e == hipSuccess) e = hipEventCreate(&c->t0);
     if (e == hipSuccess) e = hipEventCreate(&c->t1);
     if (e != hipSuccess) {
@@ -629,6 +648,15 @@ int bchip_rope_append_attention(bchip_ctx* c, float* q, const float* k, const fl
     if (!c) return fail(BCHIP_E_ARG, "no context");
     return fused_step(c, c->ws, q, k, v, kc, vc, kv_type, inv_freq, positions, nh, nkv, hd, rope_dim, neox, pos,
                       scale, out);
+}
+
+int bchip_rope_append_attention_noalloc(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc,
+                                        uint32_t kv_type, const float* inv_freq, const uint32_t* positions,
+                                        uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox,
+                                        uint32_t pos, float scale, float* out) {
+    if (!c) return fail(BCHIP_E_ARG, "no context");
+    return fused_step(c, c->fixed_ws, q, k, v, kc, vc, kv_type, inv_freq, positions, nh, nkv, hd, rope_dim, neox,
+                      pos, scale, out);
 }
 
 int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const void* vc, uint32_t kv_type,

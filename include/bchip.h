@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BCHIP_ABI_VERSION 3
+#define BCHIP_ABI_VERSION 4
 
 enum bchip_type { BCHIP_F32 = 0, BCHIP_F16 = 1 }; /* T_F32 / T_F16 of kernels.h:14-15 */
 
@@ -160,6 +160,22 @@ int bchip_rope_append_attention(bchip_ctx* ctx, float* q, const float* k, const 
                                 uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,
                                 uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos,
                                 float scale, float* out);
+
+/* bchip_rope_append_attention that allocates nothing. It has no counterpart in the
+ * reference; it is for callers that cannot allocate device memory mid-run (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). Same arguments and
+ * the same results, bit for bit. Its scratch (a step's chunk states and the staged rotated q)
+ * is a fixed array in device memory, one copy per device from the library's load until the
+ * process ends: 16 MiB of chunk states (a one-row plan of at most 1024 units x 16 slots x 256
+ * dims: any plan with n_head_kv <= 1024), 128 KiB of their maxima and sums, 256 KiB of q
+ * (nh * hd <= 65536 for the fused kernel). A step that needs more is refused with BCHIP_E_ARG
+ * before anything is launched; an f32 cache never needs more (its pass then runs unsplit, the
+ * same bits). Every call on one device shares that array, so calls on one device that overlap
+ * in time (from several contexts, threads or streams) race. */
+int bchip_rope_append_attention_noalloc(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc,
+                                        void* vc, uint32_t kv_type, const float* inv_freq,
+                                        const uint32_t* positions, uint32_t nh, uint32_t nkv, uint32_t hd,
+                                        uint32_t rope_dim, uint32_t neox, uint32_t pos, float scale, float* out);
 
 /* Several conversations' one-token steps in one launch (the reference runs one
  * k_attention per KV stream, crates/bc-mesh/src/engine.rs:25,305-309): sequence i's row
