@@ -8,7 +8,8 @@ k_attention of the reference's per-layer sequence, the same bits as bchip_rope_a
 bchip_attention); value = tokens/s of those steps, inputs resident in HBM. Extras: decode
 at 1024 and 4096 slots (their 32 layers' caches fit the 256 MB MALL: labelled so), causal
 prefill at 2048 and 8192 tokens (TFLOP/s, configs[2]), the Llama-3-70B stage share's
-prefill and verify steps, Qwen2.5-7B ragged batched decode.
+prefill and verify steps, Qwen2.5-7B ragged batched decode with each
+conversation's RoPE and K/V append in the same launch.
 
 roofline: the dominant kernel, the decode attention kernel (attn_decode_row): algorithmic
 bytes per launch (2 * L * n_kv * hd * 2 bytes of f16 K and V, each read once) over its mean
@@ -21,7 +22,8 @@ rocprofv3 counter summary.
 cpu_baseline: bc-infer's CPU attention as the oracle's C restatement (single thread, as
 the reference runs it: crates/bc-infer/src/model.rs:391-403, 448-481), timed on this
 host on a bounded sample of the same workload: a few layers of one decode token at 32768
-slots, median per layer, scaled to tokens/s for 32 layers.
+slots, median per layer, scaled to tokens/s for 32 layers. extra.cpu_per_config holds the
+same baseline beside every other configuration (each on a stated bounded sample).
 """
 import argparse
 import ctypes
@@ -236,11 +238,14 @@ def bench_multirow(ctx, hip, rows, pos, nh, nkv, hd, reps, n_layer=1, verify=Fal
 
 
 def bench_ragged(ctx, hip, reps):
-    """16 sequences, lengths U[1024, 32768] (seeded), 28/4 heads, hd 128, one
-    launch per layer over a ragged pool, 28 layers."""
-    nh, nkv, hd, n_layer = 28, 4, 128, 28
+    """16 conversations in one pool, lengths U[1024, 32768] (seeded) counting the new
+    token, 28/4 heads, hd 128, RoPE theta 1e6 (neox), 28 layers. A step is one token of every
+    conversation through every layer, each layer one bchip_rope_append_attention_ragged call:
+    the RoPE of each conversation's new q and k, its K/V append at its last slot and the
+    attention of all 16, in one launch."""
+    nh, nkv, hd, n_layer, nseq = 28, 4, 128, 28, 16
     rng = np.random.default_rng(4)
-    lens = rng.integers(1024, 32769, size=16).astype(np.uint32)
+    lens = rng.integers(1024, 32769, size=nseq).astype(np.uint32)
     offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
     total = int(lens.sum())
     kvd = nkv * hd
@@ -251,11 +256,23 @@ def bench_ragged(ctx, hip, reps):
         ctx.fill_normal(v, bchip.F16, total * kvd, 301 + 2 * layer)
         kcs.append(k)
         vcs.append(v)
-    q = ctx.zeros(16 * nh * hd * 4)
-    ctx.fill_normal(q, bchip.F32, 16 * nh * hd, 299)
-    out = ctx.zeros(16 * nh * hd * 4)
+    per = nseq * (nh + 2 * nkv) * hd  # q [16][nh*hd], then k and v [16][kvd], per layer
+    qkv = ctx.zeros(n_layer * per * 4)
+    ctx.fill_normal(qkv, bchip.F32, n_layer * per, 299)
+    pos = ctx.upload(lens - 1)
+    inv = ctx.upload(np.array([1e6 ** (-2.0 * i / hd) for i in range(hd // 2)], np.float32))
+    out = ctx.zeros(nseq * nh * hd * 4)
+    scale = 1.0 / math.sqrt(hd)
+
+    def call(layer):
+        q = qkv.ptr + layer * per * 4
+        k = q + nseq * nh * hd * 4
+        v = k + nseq * kvd * 4
+        ctx.rope_append_attention_ragged(q, k, v, kcs[layer], vcs[layer], bchip.F16, inv, pos, lens, offs, nh, nkv,
+                                         hd, hd, True, scale, out)
+
     for layer in range(n_layer):
-        ctx.attention_ragged(q, kcs[layer], vcs[layer], bchip.F16, out, lens, offs, nh, nkv, hd, 0.0884)
+        call(layer)
     ctx.sync()
     # Call figure: the timed region's stream time over the calls; the main kernel's events are
     # armed on every EVENT_EVERY-th call only (as in bench_decode).
@@ -268,19 +285,20 @@ def bench_ragged(ctx, hip, reps):
             if j % EVENT_EVERY == 0:
                 k = 2 * (j // EVENT_EVERY)
                 ctx.timer_arm(evs[k], evs[k + 1])
-            ctx.attention_ragged(q, kcs[layer], vcs[layer], bchip.F16, out, lens, offs, nh, nkv, hd, 0.0884)
+            call(layer)
             j += 1
     total_ms = ctx.timer_stop()
     per_call = [total_ms / (reps * n_layer)]
     per_kernel = [hip.elapsed(evs[2 * k], evs[2 * k + 1]) for k in range(len(armed))]
     hip.destroy(evs)
-    for b in kcs + vcs + [q, out]:
+    for b in kcs + vcs + [qkv, pos, inv, out]:
         b.free()
     us = statistics.fmean(per_kernel) * 1e3
     call_us = statistics.fmean(per_call) * 1e3
     bytes_ = 2.0 * total * kvd * 2
-    return {"seqs": 16, "total_slots": total, "layers": n_layer, "kernel_us": us, "call_us": call_us,
-            "ms_per_step": total_ms / reps, "tokens_per_s": 16 * reps / (total_ms * 1e-3),
+    return {"seqs": nseq, "total_slots": total, "layers": n_layer, "step": "bchip_rope_append_attention_ragged",
+            "kernel_us": us, "call_us": call_us, "ms_per_step": total_ms / reps,
+            "tokens_per_s": nseq * reps / (total_ms * 1e-3),
             "GBps": bytes_ / (us * 1e-6) / 1e9, "hbm_frac": bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "call_GBps": bytes_ / (call_us * 1e-6) / 1e9,
             "call_hbm_frac": bytes_ / (call_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
@@ -380,6 +398,86 @@ def cpu_baseline(layers=5, ctx_len=32768, nh=32, nkv=8, hd=128):
             "cpu": _cpu_model(), "nproc": os.cpu_count()}
 
 
+def cpu_per_config():
+    """bc-infer's CPU attention (the oracle's C restatement of model.rs:391-403, 448-481, one
+    thread, as the reference runs it) beside every configuration, each timed on this host on a
+    bounded sample and scaled by its count of (query, key) pairs or of layers, as stated in each
+    entry's "sample"."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    O.lib()
+    rng = np.random.default_rng(11)
+    out = {}
+
+    def rnd(*shape):
+        return rng.standard_normal(shape, dtype=np.float32)
+
+    # configs[0]: Qwen2.5-0.5B decode at 512 slots, f32, 24 layers: the whole workload.
+    nh, nkv, hd, L = 14, 2, 64, 512
+    inv = O.inv_freq(hd, 1e6)
+    t = 0.0
+    for layer in range(24):
+        q, kc, vc = rnd(1, nh, hd), rnd(L, nkv * hd), rnd(L, nkv * hd)
+        t0 = time.perf_counter()
+        qr = O.rope(q, nh, hd, hd, True, L - 1, inv)
+        kc[L - 1] = O.rope(kc[L - 1], nkv, hd, hd, True, L - 1, inv)
+        O.attention(qr, kc, vc, 1, L - 1, nh, nkv, hd, 0.125)
+        t += time.perf_counter() - t0
+    out["configs0_qwen05b_decode_512"] = {"tokens_per_s": 1.0 / t, "ms_per_token": t * 1e3, "cores": 1,
+                                          "sample": "the whole workload: 24 layers of one token (rope + attention)"}
+
+    def prefill(S, nh, nkv, hd, stride, name, layers):
+        # Rows r = stride-1, 2*stride-1, ... of one layer, one row a call (row r sees r+1 slots);
+        # scaled by the (query, key) pairs of all S rows.
+        q, kc, vc = rnd(S, nh, hd), rnd(S, nkv * hd), rnd(S, nkv * hd)
+        rows = list(range(stride - 1, S, stride))
+        t0 = time.perf_counter()
+        for r in rows:
+            O.attention(q[r:r + 1], kc, vc, 1, r, nh, nkv, hd, 1.0 / math.sqrt(hd))
+        t = time.perf_counter() - t0
+        per_pair = t / sum(r + 1 for r in rows)
+        res = {}
+        for s_full in ((S,) if name != "configs2_llama8b_prefill" else (2048, 8192)):
+            pairs = s_full * (s_full + 1) / 2
+            layer_s = per_pair * pairs
+            res[f"S{s_full}"] = {"s_per_layer": layer_s, "TFLOPs": 4.0 * hd * nh * pairs / layer_s / 1e12,
+                                 "tokens_per_s": s_full / (layer_s * layers)}
+        res.update({"cores": 1, "sample": f"{len(rows)} rows (every {stride}th) of one {S}-row layer, "
+                                          f"{nh}/{nkv} heads; time per (query, key) pair scaled to every row and "
+                                          f"{layers} layers" + ("; S=8192 extrapolated from S=2048's per-pair time"
+                                                                if S == 2048 else "")})
+        out[name] = res
+
+    prefill(2048, 32, 8, 128, 8, "configs2_llama8b_prefill", 32)
+    prefill(4096, 64, 8, 128, 32, "configs4_llama70b_prefill", 20)
+
+    # configs[3]: 16 conversations' one-token steps; 4 of them timed, scaled by slots.
+    nh, nkv, hd = 28, 4, 128
+    lens = np.random.default_rng(4).integers(1024, 32769, size=16)
+    picked = [int(x) for x in lens[:4]]
+    t = 0.0
+    for L in picked:
+        q, kc, vc = rnd(1, nh, hd), rnd(L, nkv * hd), rnd(L, nkv * hd)
+        t0 = time.perf_counter()
+        O.attention(q, kc, vc, 1, L - 1, nh, nkv, hd, 1.0 / math.sqrt(hd))
+        t += time.perf_counter() - t0
+    layer_s = t * float(lens.sum()) / sum(picked)
+    out["configs3_qwen7b_ragged"] = {"s_per_layer": layer_s, "tokens_per_s": 16 / (layer_s * 28), "cores": 1,
+                                     "sample": "4 of the 16 conversations, one layer, scaled by slots to all 16 and 28 "
+                                               "layers"}
+    # configs[4]: one verify step of 8 rows at 4096 slots, one layer, scaled to 20 layers.
+    nh, nkv, hd, ctx0 = 64, 8, 128, 4096
+    q, kc, vc = rnd(8, nh, hd), rnd(ctx0 + 8, nkv * hd), rnd(ctx0 + 8, nkv * hd)
+    t0 = time.perf_counter()
+    O.attention(q, kc, vc, 8, ctx0, nh, nkv, hd, 1.0 / math.sqrt(hd))
+    layer_s = time.perf_counter() - t0
+    out["configs4_llama70b_verify_4096"] = {"s_per_layer_step": layer_s, "tokens_per_s": 8 / (layer_s * 20),
+                                            "cores": 1, "sample": "one layer of one 8-row verify step at 4096 slots, "
+                                                                  "scaled to 20 layers (all 8 drafts accepted)"}
+    return out
+
+
 def profiled_traffic(ctx_len):
     """HBM bytes per decode attention call (decode + fold kernels) from the committed counter
     summary: FETCH_SIZE and WRITE_SIZE passes of rocprofv3 over this script, scaled by the
@@ -465,6 +563,8 @@ def main():
         log("cpu baseline (oracle, 1 thread)")
         cpu = cpu_baseline()
         log(json.dumps(cpu))
+        extra["cpu_per_config"] = cpu_per_config()
+        log(json.dumps(extra["cpu_per_config"]))
     if head is None:
         print(json.dumps({"extra": extra, "cpu_baseline": cpu}))
         return

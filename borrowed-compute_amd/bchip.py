@@ -81,6 +81,9 @@ def lib() -> ctypes.CDLL:
         "bchip_rope_append_attention_noalloc": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32,
                                                  P], i32),
         "bchip_attention_ragged": ([P, P, P, P, u32, P, P, P, u32, u32, u32, u32, f32], i32),
+        "bchip_rope_append_ragged": ([P, P, P, P, P, P, u32, P, P, P, P, u32, u32, u32, u32, u32, u32], i32),
+        "bchip_rope_append_attention_ragged": ([P, P, P, P, P, P, u32, P, P, P, P, u32, u32, u32, u32, u32, u32, f32,
+                                                P], i32),
         "bchip_fill_normal": ([P, P, u32, u64, u64], i32),
         "bchip_matmul": ([P, P, u32, P, P, u32, u32, u32], i32),
         "bchip_rms_norm": ([P, P, P, P, u32, u32, f32], i32),
@@ -242,6 +245,25 @@ class Ctx:
         check(lib().bchip_attention_ragged(self.h, _ptr(q), _ptr(kc), _ptr(vc), kv_type, _ptr(out),
                                            lens.ctypes.data_as(ctypes.c_void_p),
                                            offs.ctypes.data_as(ctypes.c_void_p), len(lens), nh, nkv, hd, scale))
+
+    def rope_append_ragged(self, q, k, v, kc, vc, kv_type, inv_freq, positions, seq_lens, kv_offsets, nh, nkv, hd,
+                           rope_dim, neox) -> None:
+        lens = np.ascontiguousarray(seq_lens, np.uint32)
+        offs = np.ascontiguousarray(kv_offsets, np.uint64)
+        check(lib().bchip_rope_append_ragged(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc), kv_type,
+                                             _ptr(inv_freq), _ptr(positions), lens.ctypes.data_as(ctypes.c_void_p),
+                                             offs.ctypes.data_as(ctypes.c_void_p), len(lens), nh, nkv, hd, rope_dim,
+                                             int(neox)))
+
+    def rope_append_attention_ragged(self, q, k, v, kc, vc, kv_type, inv_freq, positions, seq_lens, kv_offsets, nh,
+                                     nkv, hd, rope_dim, neox, scale, out) -> None:
+        lens = np.ascontiguousarray(seq_lens, np.uint32)
+        offs = np.ascontiguousarray(kv_offsets, np.uint64)
+        check(lib().bchip_rope_append_attention_ragged(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc),
+                                                       kv_type, _ptr(inv_freq), _ptr(positions),
+                                                       lens.ctypes.data_as(ctypes.c_void_p),
+                                                       offs.ctypes.data_as(ctypes.c_void_p), len(lens), nh, nkv, hd,
+                                                       rope_dim, int(neox), scale, _ptr(out)))
 
     def matmul(self, w, wtype, x, out, rows, cols, n) -> None:
         check(lib().bchip_matmul(self.h, _ptr(w), wtype, _ptr(x), _ptr(out), rows, cols, n))

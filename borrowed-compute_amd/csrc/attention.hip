@@ -554,7 +554,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     uint32_t it = 0;
     while (it + 1 < p.nitems && u >= p.items[it + 1].unit0) it++;
     const Item I = p.items[it];
-    const uint32_t pos0 = FUSE ? p.positions[0] : 0u;  // before any store: a scalar load
+    const uint32_t pos0 = FUSE ? p.positions[I.row] : 0u;  // before any store: a scalar load
     const uint32_t hd = p.hd, kvd = p.nkv * hd, G = p.G;
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = rem % p.nkv;
     const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, I.len);
@@ -640,8 +640,9 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
             qf[i] = *(const f32x4*)(e < G * hd ? qg + e : zf);
         }
         const bool nk = has_new && 4 * (uint32_t)lane < hd;
-        kf = *(const f32x4*)(nk ? p.knew + (size_t)kvh * hd + 4 * lane : zf);
-        vf = *(const f32x4*)(nk ? p.vnew + (size_t)kvh * hd + 4 * lane : zf);
+        const size_t kvrow = ((size_t)I.row * p.nkv + kvh) * hd + 4 * lane;
+        kf = *(const f32x4*)(nk ? p.knew + kvrow : zf);
+        vf = *(const f32x4*)(nk ? p.vnew + kvrow : zf);
     } else {
 #pragma unroll
         for (int j = 0; j < NLE; j++) {
@@ -748,10 +749,12 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
             qb[c2] = ok ? h : half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
         // q stays rotated, as k_rope leaves it. Other units of this KV head may still be
-        // reading it, so with several chunks the first one stages the rotated heads and
-        // attn_row_fold, which runs after every unit, copies them into q; a lone unit writes q.
+        // reading it, so with several chunks the first one stages the rotated heads (at the
+        // item's place in qrot) and attn_row_fold, which runs after every unit, copies them
+        // into q; a lone unit writes q.
         if (c == 0) {
-            float* dst = (I.nchunk == 1 ? p.qw + (size_t)I.row * p.nh * hd : p.qrot) + (size_t)kvh * G * hd;
+            float* dst = (I.nchunk == 1 ? p.qw + (size_t)I.row * p.nh * hd : p.qrot + (size_t)it * p.nh * hd) +
+                         (size_t)kvh * G * hd;
             for (uint32_t e = 4 * lane; e < G * hd; e += 256)
                 *(f32x4*)&dst[e] = *(const f32x4*)__builtin_assume_aligned(&qs[e], 16);
         }
@@ -923,7 +926,8 @@ __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectPa
     __shared__ float4 rO[R][D4];
     __shared__ float2 rML[R][D4];
     const uint32_t b = blockIdx.x / NDS, ds = blockIdx.x % NDS, per_item = p.nkv * p.G;
-    const Item I = p.items[b / per_item];
+    const uint32_t item = b / per_item;
+    const Item I = p.items[item];
     const uint32_t nch = I.nchunk;
     if (nch <= 1) return;  // written by the decode kernel
     const uint32_t kvh = (b % per_item) / p.G, s = (b % per_item) % p.G;
@@ -931,7 +935,7 @@ __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectPa
     if (p.fuse && tid < ROW_FOLD_DIMS && ds * ROW_FOLD_DIMS + tid < p.hd) {
         // A fused step: every unit has read q; leave head kvh * G + s rotated.
         const size_t h = (size_t)kvh * p.G + s, e = ds * ROW_FOLD_DIMS + tid;
-        p.qw[((size_t)I.row * p.nh + h) * p.hd + e] = p.qrot[h * p.hd + e];
+        p.qw[((size_t)I.row * p.nh + h) * p.hd + e] = p.qrot[((size_t)item * p.nh + h) * p.hd + e];
     }
     const size_t cu0 = (size_t)I.unit0 + (size_t)kvh * nch;
     float2 ml[NPT];
@@ -1668,6 +1672,12 @@ hipError_t row_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& 
     return row_launch(a, &item, 1, &r, ws, s);
 }
 
+hipError_t row_attention_fused_items(const AttnCall& a, const RopeArgs& r, const Item* items, uint32_t nitems,
+                                     Workspace& ws, hipStream_t s) {
+    if (!row_fusable(a.nh, a.nkv, a.hd, r.rope_dim, r.neox)) return hipErrorInvalidValue;
+    return row_launch(a, items, nitems, &r, ws, s);
+}
+
 static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nitems, const RopeArgs* rope,
                              Workspace& ws, hipStream_t s) {
     if (nitems == 0 || nitems > MAX_ITEMS) return hipErrorInvalidValue;
@@ -1700,7 +1710,7 @@ static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nite
     dp.nunits = (uint32_t)units;
     const int hdp = pad_hd(a.hd);
     hipError_t e = ws.reserve((size_t)units * 16, (size_t)hdp);
-    if (e == hipSuccess && rope) e = ws.reserve_qrot((size_t)a.nh * a.hd);
+    if (e == hipSuccess && rope) e = ws.reserve_qrot((size_t)nitems * a.nh * a.hd);
     if (e != hipSuccess) return e;
     dp.part_o = ws.o;
     dp.part_ml = ws.ml;

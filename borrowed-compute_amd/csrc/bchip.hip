@@ -659,30 +659,28 @@ int bchip_rope_append_attention_noalloc(bchip_ctx* c, float* q, const float* k, 
                       pos, scale, out);
 }
 
-int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const void* vc, uint32_t kv_type,
-                           float* out, const uint32_t* seq_lens, const uint64_t* kv_offsets, uint32_t nseq,
-                           uint32_t nh, uint32_t nkv, uint32_t hd, float scale) {
-    CHECK(enter(c));
-    if (nseq == 0) return BCHIP_OK;
-    if (!q || !kc || !vc || !out || !seq_lens || !kv_offsets) return fail(BCHIP_E_ARG, "null pointer");
-    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+// Checks shared by the ragged calls: every sequence sees at least one slot, and its slots
+// lie inside both caches.
+static int check_ragged(bchip_ctx* c, const void* kc, const void* vc, uint32_t kv_type, const uint32_t* seq_lens,
+                        const uint64_t* kv_offsets, uint32_t nseq, uint64_t kvd) {
     if (nseq > 256) return fail(BCHIP_E_ARG, "%u sequences (at most 256)", nseq);
-    CHECK(check_heads(nh, nkv, hd));
-    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc))
-        return fail(BCHIP_E_ARG, "q, out and the caches must be 16-byte aligned");
-    const uint64_t kvd = (uint64_t)nkv * hd;
-    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
-    CHECK(check_span(c, out, (uint64_t)nseq * nh * hd * 4, "out"));
     for (uint32_t i = 0; i < nseq; i++) {
         if (seq_lens[i] == 0) return fail(BCHIP_E_ARG, "sequence %u sees no slots", i);
         const uint64_t end = (kv_offsets[i] + seq_lens[i]) * kvd * esize(kv_type);
         CHECK(check_span(c, kc, end, "kc"));
         CHECK(check_span(c, vc, end, "vc"));
     }
-    const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
-    AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, 0u, scale, limit};
-    c->take_marks(a);
-    if (kv_type == BCHIP_F32) {
+    return BCHIP_OK;
+}
+
+// The attention of a ragged batch, arguments checked: sequence i's row of q against its
+// seq_lens[i] slots from kv_offsets[i].
+static int ragged_attention(bchip_ctx* c, AttnCall& a, const uint32_t* seq_lens, const uint64_t* kv_offsets,
+                            uint32_t nseq) {
+    const float* q = a.q;
+    float* out = a.out;
+    const uint32_t nh = a.nh, nkv = a.nkv, hd = a.hd;
+    if (a.kv_type == BCHIP_F32) {
         // One f32-path call per sequence, each at its place in the pool, its result the bits of
         // the sequence alone. The workspace is sized for the longest first, so that no call
         // reallocates it while an earlier one may still read it.
@@ -712,6 +710,106 @@ int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const v
             I.kvoff = kv_offsets[s0 + i];
         }
         HIP_TRY(row_attention(a, items, ns, c->ws, c->stream), "ragged attention");
+        a.ev_before = a.ev_after = nullptr;  // the events mark the first launch only
+    }
+    return BCHIP_OK;
+}
+
+int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const void* vc, uint32_t kv_type,
+                           float* out, const uint32_t* seq_lens, const uint64_t* kv_offsets, uint32_t nseq,
+                           uint32_t nh, uint32_t nkv, uint32_t hd, float scale) {
+    CHECK(enter(c));
+    if (nseq == 0) return BCHIP_OK;
+    if (!q || !kc || !vc || !out || !seq_lens || !kv_offsets) return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    CHECK(check_heads(nh, nkv, hd));
+    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc))
+        return fail(BCHIP_E_ARG, "q, out and the caches must be 16-byte aligned");
+    const uint64_t kvd = (uint64_t)nkv * hd;
+    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
+    CHECK(check_span(c, out, (uint64_t)nseq * nh * hd * 4, "out"));
+    CHECK(check_ragged(c, kc, vc, kv_type, seq_lens, kv_offsets, nseq, kvd));
+    const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
+    AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, 0u, scale, limit};
+    c->take_marks(a);
+    return ragged_attention(c, a, seq_lens, kv_offsets, nseq);
+}
+
+int bchip_rope_append_ragged(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc,
+                             uint32_t kv_type, const float* inv_freq, const uint32_t* positions,
+                             const uint32_t* seq_lens, const uint64_t* kv_offsets, uint32_t nseq, uint32_t nh,
+                             uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox) {
+    CHECK(enter(c));
+    if (nseq == 0) return BCHIP_OK;
+    if (!q || !k || !v || !kc || !vc || !inv_freq || !positions || !seq_lens || !kv_offsets)
+        return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    if (hd % 2 || rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
+    if (nh == 0 || nkv == 0) return fail(BCHIP_E_ARG, "no heads");
+    const uint64_t kvd = (uint64_t)nkv * hd;
+    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
+    CHECK(check_span(c, k, nseq * kvd * 4, "k"));
+    CHECK(check_span(c, v, nseq * kvd * 4, "v"));
+    CHECK(check_span(c, positions, (uint64_t)nseq * 4, "positions"));
+    CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
+    CHECK(check_ragged(c, kc, vc, kv_type, seq_lens, kv_offsets, nseq, kvd));
+    std::vector<uint64_t> slots(nseq);
+    for (uint32_t i = 0; i < nseq; i++) slots[i] = kv_offsets[i] + seq_lens[i] - 1;
+    HIP_TRY(rope_append_ragged_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, nseq, nh, nkv, hd, rope_dim,
+                                      neox, slots.data(), c->stream),
+            "rope_append_ragged");
+    return BCHIP_OK;
+}
+
+int bchip_rope_append_attention_ragged(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc,
+                                       uint32_t kv_type, const float* inv_freq, const uint32_t* positions,
+                                       const uint32_t* seq_lens, const uint64_t* kv_offsets, uint32_t nseq,
+                                       uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox,
+                                       float scale, float* out) {
+    CHECK(enter(c));
+    if (nseq == 0) return BCHIP_OK;
+    if (!q || !k || !v || !kc || !vc || !inv_freq || !positions || !seq_lens || !kv_offsets || !out)
+        return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    CHECK(check_heads(nh, nkv, hd));
+    if (rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
+    const bool fuse = kv_type == BCHIP_F16 && row_fusable(nh, nkv, hd, rope_dim, neox);
+    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc) || (fuse && (!aligned16(k) || !aligned16(v))))
+        return fail(BCHIP_E_ARG, "q, k, v, out and the caches must be 16-byte aligned");
+    const uint64_t kvd = (uint64_t)nkv * hd;
+    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
+    CHECK(check_span(c, out, (uint64_t)nseq * nh * hd * 4, "out"));
+    CHECK(check_span(c, k, nseq * kvd * 4, "k"));
+    CHECK(check_span(c, v, nseq * kvd * 4, "v"));
+    CHECK(check_span(c, positions, (uint64_t)nseq * 4, "positions"));
+    CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
+    CHECK(check_ragged(c, kc, vc, kv_type, seq_lens, kv_offsets, nseq, kvd));
+    const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
+    AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, 0u, scale, limit};
+    c->take_marks(a);
+    if (!fuse) {
+        // f32 caches, and shapes the fused kernel does not take: the two calls.
+        std::vector<uint64_t> slots(nseq);
+        for (uint32_t i = 0; i < nseq; i++) slots[i] = kv_offsets[i] + seq_lens[i] - 1;
+        HIP_TRY(rope_append_ragged_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, nseq, nh, nkv, hd,
+                                          rope_dim, neox, slots.data(), c->stream),
+                "rope_append_ragged");
+        return ragged_attention(c, a, seq_lens, kv_offsets, nseq);
+    }
+    RopeArgs r{q, k, v, inv_freq, positions, rope_dim, neox};
+    for (uint32_t s0 = 0; s0 < nseq; s0 += MAX_ITEMS) {
+        const uint32_t ns = std::min<uint32_t>(MAX_ITEMS, nseq - s0);
+        Item items[MAX_ITEMS];
+        for (uint32_t i = 0; i < ns; i++) {
+            Item& I = items[i];
+            I = Item{};
+            I.row = s0 + i;
+            I.nrows = 1;
+            I.len = seq_lens[s0 + i];
+            I.kvoff = kv_offsets[s0 + i];
+        }
+        HIP_TRY(row_attention_fused_items(a, r, items, ns, c->ws, c->stream), "rope_append_attention_ragged");
+        a.ev_before = a.ev_after = nullptr;
     }
     return BCHIP_OK;
 }

@@ -63,6 +63,10 @@ struct RopeArgs {
     uint32_t rope_dim, neox;
 };
 hipError_t row_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s);
+// Several sequences' fused steps in one launch: item i is row items[i].row of q, k, v, out and
+// positions, its cache at items[i].kvoff with items[i].len slots, the new row the last.
+hipError_t row_attention_fused_items(const AttnCall& a, const RopeArgs& r, const Item* items, uint32_t nitems,
+                                     Workspace& ws, hipStream_t s);
 bool row_fusable(uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox);
 // Workspace slots (chunk states) a one-row call over a list of len entries takes.
 size_t row_state_slots(uint64_t len, uint32_t nkv);
@@ -82,6 +86,12 @@ hipError_t rope_append_launch(float* q, const float* k, const float* v, void* kc
                               const float* inv_freq, const uint32_t* positions, uint32_t rows, uint32_t nh,
                               uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint64_t slot0,
                               hipStream_t s);
+// Row r of q, k, v to cache slot slots[r] (host array): one new row of each of several
+// sequences in one pool.
+hipError_t rope_append_ragged_launch(float* q, const float* k, const float* v, void* kc, void* vc, uint32_t kv_type,
+                                     const float* inv_freq, const uint32_t* positions, uint32_t rows, uint32_t nh,
+                                     uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox,
+                                     const uint64_t* slots, hipStream_t s);
 hipError_t copy_launch(const void* src, uint32_t st, void* dst, uint32_t dt, uint64_t off, uint64_t n, hipStream_t s);
 hipError_t move_launch(void* buf, uint32_t type, uint64_t from, uint64_t to, uint64_t n, hipStream_t s);
 hipError_t keep_launch(void* const* bufs, uint32_t nbufs, uint32_t type, uint32_t width, uint64_t base,

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BCHIP_ABI_VERSION 4
+#define BCHIP_ABI_VERSION 5
 
 enum bchip_type { BCHIP_F32 = 0, BCHIP_F16 = 1 }; /* T_F32 / T_F16 of kernels.h:14-15 */
 
@@ -188,6 +188,28 @@ int bchip_attention_ragged(bchip_ctx* ctx, const float* q, const void* kc, const
                            uint32_t kv_type, float* out, const uint32_t* seq_lens,
                            const uint64_t* kv_offsets, uint32_t nseq, uint32_t nh,
                            uint32_t nkv, uint32_t hd, float scale);
+
+/* The append of one new row to each of several conversations in one cache pool, as one
+ * launch (the reference keeps up to 16 conversations' caches a stage and appends each with
+ * its own k_rope and k_copy, crates/bc-mesh/src/engine.rs:25, 305-314, gpu/mod.rs:464-475):
+ * sequence i's q row [nh][hd] and k row [nkv][hd] turn by positions[i] (device u32 [nseq];
+ * normally seq_lens[i] - 1), and k and v go into slot kv_offsets[i] + seq_lens[i] - 1 of kc and
+ * vc, its last visible slot. seq_lens, kv_offsets: host arrays; nseq <= 256; sequences' slots
+ * must not overlap. Each row's bits are those of bchip_rope_append with rows = 1 at that slot. */
+int bchip_rope_append_ragged(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
+                             uint32_t kv_type, const float* inv_freq, const uint32_t* positions,
+                             const uint32_t* seq_lens, const uint64_t* kv_offsets, uint32_t nseq, uint32_t nh,
+                             uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox);
+
+/* One decode step of several conversations: bchip_rope_append_ragged, then
+ * bchip_attention_ragged over the same seq_lens and kv_offsets, with the same results bit for
+ * bit; for f16 caches and the shapes bchip_rope_append_attention fuses, one launch does the
+ * rotations, the appends and the attention of every sequence (at most 64 a launch). */
+int bchip_rope_append_attention_ragged(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc,
+                                       void* vc, uint32_t kv_type, const float* inv_freq,
+                                       const uint32_t* positions, const uint32_t* seq_lens,
+                                       const uint64_t* kv_offsets, uint32_t nseq, uint32_t nh, uint32_t nkv,
+                                       uint32_t hd, uint32_t rope_dim, uint32_t neox, float scale, float* out);
 
 /* ---- The rest of a layer (Layers::forward, mod.rs:454-491): the GGUF block-format
  * product, RMSNorm and the elementwise ops. Weight types are ggml's numbers
