@@ -85,6 +85,7 @@ def lib() -> ctypes.CDLL:
         "bchip_rope_append_attention_ragged": ([P, P, P, P, P, P, u32, P, P, P, P, u32, u32, u32, u32, u32, u32, f32,
                                                 P], i32),
         "bchip_fill_normal": ([P, P, u32, u64, u64], i32),
+        "bchip_sample": ([P, P, u32, u32, f32, f32, u64, u64, P], i32),
         "bchip_matmul": ([P, P, u32, P, P, u32, u32, u32], i32),
         "bchip_rms_norm": ([P, P, P, P, u32, u32, f32], i32),
         "bchip_bias_add": ([P, P, P, u64, u32], i32),
@@ -279,6 +280,11 @@ class Ctx:
 
     def add(self, x, y, n) -> None:
         check(lib().bchip_add(self.h, _ptr(x), _ptr(y), n))
+
+    def sample(self, scores, rows, vocab, temperature, top_p, seed, step0, ids) -> None:
+        """sample.rs on the device: ids (device u32 [rows]) from scores (device f32 [rows][vocab])."""
+        check(lib().bchip_sample(self.h, _ptr(scores), rows, vocab, temperature, top_p, seed & 0xFFFFFFFFFFFFFFFF,
+                                 step0 & 0xFFFFFFFFFFFFFFFF, _ptr(ids)))
 
     def fill_normal(self, dst, t, n, seed) -> None:
         check(lib().bchip_fill_normal(self.h, _ptr(dst), t, n, seed))

@@ -814,6 +814,26 @@ int bchip_rope_append_attention_ragged(bchip_ctx* c, float* q, const float* k, c
     return BCHIP_OK;
 }
 
+int bchip_sample(bchip_ctx* c, const float* scores, uint32_t rows, uint32_t vocab, float temperature, float top_p,
+                 uint64_t seed, uint64_t step0, uint32_t* ids) {
+    CHECK(enter(c));
+    if (rows == 0) return BCHIP_OK;
+    if (!scores || !ids) return fail(BCHIP_E_ARG, "null pointer");
+    if (vocab == 0) return fail(BCHIP_E_ARG, "an empty vocabulary");
+    if (rows > 65535) return fail(BCHIP_E_ARG, "%u rows (at most 65535 a call)", rows);
+    CHECK(check_span(c, scores, (uint64_t)rows * vocab * 4, "scores"));
+    CHECK(check_span(c, ids, (uint64_t)rows * 4, "ids"));
+    size_t need = 0;
+    if (temperature > 0.0f) {
+        need = sample_scratch_bytes(rows, vocab);
+        HIP_TRY(c->ws.reserve_vt(need), "sampler scratch");
+    }
+    HIP_TRY(sample_launch(scores, rows, vocab, temperature, top_p, seed, step0, ids, c->ws.vt, c->ws.vt_bytes,
+                          c->stream),
+            "sample");
+    return BCHIP_OK;
+}
+
 int bchip_fill_normal(bchip_ctx* c, void* dst, uint32_t type, uint64_t n, uint64_t seed) {
     CHECK(enter(c));
     if (n == 0) return BCHIP_OK;

@@ -16,7 +16,7 @@ struct Workspace {
     float* o = nullptr;    // [units*slots][hd_pad]: chunk states
     float* ml = nullptr;   // [units*slots][2]
     void* zero = nullptr;  // ZERO_BYTES of zeros
-    void* vt = nullptr;    // V^T tiles of a prefill call
+    void* vt = nullptr;    // V^T tiles of a prefill call; the sampler's keys and sort scratch
     float* qrot = nullptr;  // rotated q of a fused step, until attn_row_fold copies it
     size_t slots = 0, hdp = 0, vt_bytes = 0, qrot_floats = 0;
     bool fixed = false;
@@ -99,6 +99,13 @@ hipError_t keep_launch(void* const* bufs, uint32_t nbufs, uint32_t type, uint32_
 hipError_t grow_launch(const void* const* src, void* const* dst, uint32_t nbufs, uint64_t keep_bytes,
                        uint64_t total_bytes, hipStream_t s);
 hipError_t fill_normal_launch(void* dst, uint32_t type, uint64_t n, uint64_t seed, hipStream_t s);
+
+// The sampler (sample.hip): ids[r] = sample.rs's pick for row r of scores [rows][vocab] at step
+// step0 + r. scratch: sample_scratch_bytes(rows, vocab) bytes (unused for temperature <= 0).
+size_t sample_scratch_bytes(uint32_t rows, uint32_t vocab);
+hipError_t sample_launch(const float* scores, uint32_t rows, uint32_t vocab, float temperature, float top_p,
+                         uint64_t seed, uint64_t step0, uint32_t* ids, void* scratch, size_t scratch_bytes,
+                         hipStream_t s);
 
 // The rest of a layer (layer.hip).
 bool ggml_block(uint32_t type, uint32_t& weights, uint32_t& bytes);

@@ -1,6 +1,7 @@
 """One pipeline stage's layers on the GPU: bc-infer's Layers::forward
-(crates/bc-infer/src/gpu/mod.rs:428-495) and its logits head (mod.rs:499-508, the product
-of model.rs:361-370), issued as this library's entry points instead of a Cmd list.
+(crates/bc-infer/src/gpu/mod.rs:428-495), its logits head (mod.rs:499-508, the product
+of model.rs:361-370) and the sampler after it (sample.rs, engine.rs:341-350), issued as this
+library's entry points instead of a Cmd list.
 
 Per layer, in the reference's order: RMSNorm, the q/k/v products, their biases, RoPE of q
 and k with the append of k and v at slot `pos` (the four commands at mod.rs:464-475 as one
@@ -182,6 +183,27 @@ class GpuLayers:
         ctx.matmul(out, ty, s["n"], scores, upto, vc, rows)
         got = ctx.read(scores, (rows, upto))
         scores.free()
+        return got
+
+    def sample(self, x: np.ndarray, rows: int, temperature: float, top_p: float, seed: int, step0: int,
+               upto: int | None = None) -> np.ndarray:
+        """The last stage's next tokens (engine.rs:341-350): the logits head, then sample.rs's
+        pick for each row on the device (bchip_sample; row r at step step0 + r). Only the ids
+        come back to the host, not the rows x vocab scores."""
+        if self.head is None:
+            raise ValueError("this stage has no output head")
+        norm, out, ty, vr, vc = self.head
+        upto = vr if upto is None else min(upto, vr)
+        s = self._scratch(rows)
+        ctx = self.ctx
+        ctx.upload(np.ascontiguousarray(x, np.float32), s["x"])
+        ctx.rms_norm(s["x"], norm, s["n"], rows, self.cfg.n_embd, self.cfg.eps)
+        scores, ids = ctx.zeros(rows * upto * 4), ctx.zeros(rows * 4)
+        ctx.matmul(out, ty, s["n"], scores, upto, vc, rows)
+        ctx.sample(scores, rows, upto, temperature, top_p, seed, step0, ids)
+        got = ctx.read(ids, (rows,), np.uint32)
+        scores.free()
+        ids.free()
         return got
 
     def free(self) -> None:

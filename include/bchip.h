@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define BCHIP_ABI_VERSION 5
+#define BCHIP_ABI_VERSION 6
 
 enum bchip_type { BCHIP_F32 = 0, BCHIP_F16 = 1 }; /* T_F32 / T_F16 of kernels.h:14-15 */
 
@@ -250,6 +250,17 @@ int bchip_silu_mul(bchip_ctx* ctx, float* g, const float* u, uint64_t n);
 
 /* k_add (kernels.h:330, entry cuda.cu:88; mod.rs:484, 490): x[i] += y[i], i < n. */
 int bchip_add(bchip_ctx* ctx, float* x, const float* y, uint64_t n);
+
+/* sample.rs:24-71 on the device, the step after the logits head (gpu/mod.rs:499-508;
+ * engine.rs:341-350): ids[r] (device u32 [rows]) = the token picked from row r of scores
+ * (device f32 [rows][vocab]) at step step0 + r. temperature <= 0: the first index of the
+ * highest score. Otherwise p = exp((score - max) / temperature) (exp correctly rounded: the
+ * reference takes its C library's expf, equal but for arguments within 0.002 ulp of a rounding
+ * midpoint), the smallest prefix of the stable descending order whose mass reaches top_p, and
+ * the seeded draw of sample.rs:61-67 with uniform(seed ^ step * 0x9e3779b97f4a7c15). Every sum
+ * runs in the reference's order, so the ids are the reference's. rows <= 65535. */
+int bchip_sample(bchip_ctx* ctx, const float* scores, uint32_t rows, uint32_t vocab, float temperature,
+                 float top_p, uint64_t seed, uint64_t step0, uint32_t* ids);
 
 /* Seeded N(0,1) draws into dst (n elements of type): splitmix64 (Steele, Lea and Flood
  * 2014) + Box-Muller (1958), the generator of the benchmark inputs; draw i of seed s is

@@ -119,6 +119,19 @@ void bcl_silu_mul(float* g, const float* u, uint64_t n);
 void bcl_bias_add(float* x, const float* b, uint64_t n, uint64_t dim);
 void bcl_add(float* x, const float* y, uint64_t n);
 
+/* The sampler (bc_sample.c):
+ *   bcs_argmax    crates/bc-infer/src/sample.rs:24-32
+ *   bcs_uniform   crates/bc-infer/src/sample.rs:74-81 (splitmix64 one step, top 24 bits)
+ *   bcs_sample    crates/bc-infer/src/sample.rs:35-71 (temperature, top-p nucleus, seeded draw)
+ *   bcs_exp       f32::exp as the correctly rounded value (the reference leaves it to libm)
+ * Pinned by the reference's greedy_and_nucleus test (sample.rs:78-89), the published
+ * splitmix64 sequence, and properties with closed answers (tests/test_oracle_sample.py). */
+uint32_t bcs_argmax(const float* s, uint32_t n);
+float bcs_uniform(uint64_t seed);
+float bcs_exp(float x);
+uint32_t bcs_sample(const float* scores, uint32_t n, float temperature, float top_p, uint64_t seed,
+                    uint64_t step);
+
 #ifdef __cplusplus
 }
 #endif

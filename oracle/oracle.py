@@ -68,6 +68,14 @@ def lib() -> ctypes.CDLL:
         L.bcl_silu_mul.argtypes = [P, P, u64]
         L.bcl_bias_add.argtypes = [P, P, u64, u64]
         L.bcl_add.argtypes = [P, P, u64]
+        L.bcs_argmax.argtypes = [P, u32]
+        L.bcs_argmax.restype = u32
+        L.bcs_uniform.argtypes = [u64]
+        L.bcs_uniform.restype = f32
+        L.bcs_exp.argtypes = [f32]
+        L.bcs_exp.restype = f32
+        L.bcs_sample.argtypes = [P, u32, f32, f32, u64, u64]
+        L.bcs_sample.restype = u32
         _lib = L
     return _lib
 
@@ -296,3 +304,22 @@ def add(x, y) -> np.ndarray:
     xv = _f32(x).copy()
     lib().bcl_add(_p(xv), _p(_f32(y)), xv.size)
     return xv
+
+
+# ---- The sampler (bc_sample.c). ----
+def argmax(scores) -> int:
+    """sample.rs:24-32."""
+    s = _f32(scores)
+    return int(lib().bcs_argmax(_p(s), s.size))
+
+
+def uniform(seed: int) -> float:
+    """sample.rs:74-81."""
+    return float(lib().bcs_uniform(seed & 0xFFFFFFFFFFFFFFFF))
+
+
+def sample(scores, temperature: float, top_p: float, seed: int, step: int) -> int:
+    """sample.rs:35-71 (exp correctly rounded)."""
+    s = _f32(scores)
+    return int(lib().bcs_sample(_p(s), s.size, temperature, top_p, seed & 0xFFFFFFFFFFFFFFFF,
+                                step & 0xFFFFFFFFFFFFFFFF))

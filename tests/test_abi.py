@@ -17,7 +17,7 @@ def test_library_exports_every_declared_function():
     assert len(names) >= 20
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.bchip_abi_version() == 5
+    assert lib.bchip_abi_version() == 6
 
 
 def test_exported_symbols_are_exactly_the_header():

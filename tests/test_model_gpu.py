@@ -161,6 +161,22 @@ def test_a_tree_pass_scores_every_path_as_if_fed_alone(ctx, neox):
     part.g.free()
 
 
+def test_the_last_stage_samples_on_the_device(ctx):
+    """engine.rs:341-350: the last stage samples every row (sample.rs). On the device, the ids
+    equal the restatement's picks from the same stage's scores, greedy and nucleus."""
+    model = tiny_model(2, False)
+    part = Part(ctx, model, 0, 2, True)
+    kv = part.g.new_cache()
+    x = part.forward(embed(part.embd, [5, 9, 13, 2, 7]), 0, None, kv)
+    scores = part.g.logits(x, 5)
+    for temperature, top_p, seed in ((0.0, 1.0, 0), (0.8, 0.9, 42), (1.3, 1.0, 7)):
+        ids = part.g.sample(x, 5, temperature, top_p, seed, 10)
+        want = [O.sample(scores[r], temperature, top_p, seed, 10 + r) for r in range(5)]
+        np.testing.assert_array_equal(ids, want, err_msg=f"T {temperature} top_p {top_p}")
+    kv.free()
+    part.g.free()
+
+
 def test_a_long_conversation_grows_the_gpu_cache(ctx):
     """model.rs:652-675: 1100 tokens in passes of 300 (past the first 256-slot allocation
     and past one 1024-slot tile of the reference's kernel), against the exact forward."""

@@ -1,22 +1,24 @@
 """Test fixture: the reference's small random Llama-shaped model (crates/bc-infer/src/
-fixtures.rs:7-60), restated: width 64, feed-forward 128, vocabulary 96, 4 query and 2 KV
-heads, Q8_0 matrices (quantised by the oracle's restatement of quant.rs:634-646), f32
-norms and q bias, the weights drawn from one xorshift stream in the file's tensor order.
-The GGUF container is left out: the library takes each tensor's block bytes as they sit in
-the file. Also an f64 forward of the same model (model.rs:297-352 with dequantised
+fixtures.rs:7-60), restated as the same GGUF file: width 64, feed-forward 128, vocabulary 96,
+4 query and 2 KV heads, Q8_0 matrices (quantised by the oracle's restatement of
+quant.rs:634-646), f32 norms and q bias, the weights drawn from one xorshift stream in the
+file's tensor order, the metadata and tokens of fixtures.rs:38-56, written by gguf.write_gguf
+(gguf.rs:233-296) and read back by gguf.load_stage (the loader the GPU layers take their
+weights from). Also an f64 forward of the same model (model.rs:297-352 with dequantised
 weights and exact arithmetic) to check the GPU layers against."""
 from __future__ import annotations
 
 import numpy as np
 
 import oracle as O
+from gguf import load_stage, write_gguf
 from layers import Config, Matrix, inv_freq
 
 M64 = (1 << 64) - 1
 
 
-def tiny_model(n_layer: int, neox: bool):
-    """fixtures.rs:7-60: (Config, layer dicts for GpuLayers, head, embedding Matrix)."""
+def tiny_model_file(n_layer: int, neox: bool) -> bytes:
+    """fixtures.rs:7-60: the GGUF file's bytes."""
     d, ff, vocab, heads, kv_heads = 64, 128, 96, 4, 2
     state = [0x9E3779B97F4A7C15]
 
@@ -31,29 +33,42 @@ def tiny_model(n_layer: int, neox: bool):
         state[0] = s
         return out
 
-    def q8(v: np.ndarray, rows: int, cols: int) -> Matrix:
-        return Matrix(O.Q8_0, O.quantize_q8_0(v).tobytes(), rows, cols)
-
-    embd = q8(rnd(d * vocab, 1.0), vocab, d)
+    q8 = lambda v: O.quantize_q8_0(v).tobytes()
+    f32b = lambda v: np.asarray(v, "<f4").tobytes()
     kvd = d // heads * kv_heads
-    layers = []
-    for _ in range(n_layer):
-        l = {}
-        l["attn_norm"] = (rnd(d, 0.2) + np.float32(1.0)).astype(np.float32)
-        l["wq"] = q8(rnd(d * d, 0.15), d, d)
-        l["wk"] = q8(rnd(d * kvd, 0.15), kvd, d)
-        l["wv"] = q8(rnd(d * kvd, 0.15), kvd, d)
-        l["bq"] = rnd(d, 0.1)
-        l["bk"] = l["bv"] = None
-        l["wo"] = q8(rnd(d * d, 0.15), d, d)
-        l["ffn_norm"] = (rnd(d, 0.2) + np.float32(1.0)).astype(np.float32)
-        l["gate"] = q8(rnd(d * ff, 0.15), ff, d)
-        l["up"] = q8(rnd(d * ff, 0.15), ff, d)
-        l["down"] = q8(rnd(ff * d, 0.15), d, ff)
-        layers.append(l)
-    head = (np.ones(d, np.float32), q8(rnd(d * vocab, 0.3), vocab, d))
-    cfg = Config(n_embd=d, n_layer=n_layer, n_head=heads, n_head_kv=kv_heads, head_dim=d // heads,
-                 rope_dim=d // heads, rope_base=10000.0, rope_neox=neox, eps=1e-5, vocab=vocab, context=2048)
+    tensors = [("token_embd.weight", [d, vocab], 8, q8(rnd(d * vocab, 1.0)))]
+    for l in range(n_layer):
+        p = lambda s: f"blk.{l}.{s}"
+        tensors += [
+            (p("attn_norm.weight"), [d], 0, f32b(rnd(d, 0.2) + np.float32(1.0))),
+            (p("attn_q.weight"), [d, d], 8, q8(rnd(d * d, 0.15))),
+            (p("attn_k.weight"), [d, kvd], 8, q8(rnd(d * kvd, 0.15))),
+            (p("attn_v.weight"), [d, kvd], 8, q8(rnd(d * kvd, 0.15))),
+            (p("attn_q.bias"), [d], 0, f32b(rnd(d, 0.1))),
+            (p("attn_output.weight"), [d, d], 8, q8(rnd(d * d, 0.15))),
+            (p("ffn_norm.weight"), [d], 0, f32b(rnd(d, 0.2) + np.float32(1.0))),
+            (p("ffn_gate.weight"), [d, ff], 8, q8(rnd(d * ff, 0.15))),
+            (p("ffn_up.weight"), [d, ff], 8, q8(rnd(d * ff, 0.15))),
+            (p("ffn_down.weight"), [ff, d], 8, q8(rnd(ff * d, 0.15))),
+        ]
+    tensors.append(("output_norm.weight", [d], 0, f32b(np.ones(d, np.float32))))
+    tensors.append(("output.weight", [d, vocab], 8, q8(rnd(d * vocab, 0.3))))
+    arch = "qwen2" if neox else "llama"
+    tokens = ["<unk>", "<s>", "</s>"] + [chr(32 + i % 95) for i in range(vocab - 3)]
+    meta = [("general.architecture", "str", arch), ("general.name", "str", "tiny"),
+            (f"{arch}.embedding_length", "u32", d), (f"{arch}.block_count", "u32", n_layer),
+            (f"{arch}.attention.head_count", "u32", heads), (f"{arch}.attention.head_count_kv", "u32", kv_heads),
+            (f"{arch}.feed_forward_length", "u32", ff), (f"{arch}.context_length", "u32", 2048),
+            ("tokenizer.ggml.model", "str", "llama"), ("tokenizer.ggml.tokens", "strs", tokens),
+            ("tokenizer.ggml.scores", "f32s", [0.0] * vocab), ("tokenizer.ggml.bos_token_id", "u32", 1),
+            ("tokenizer.ggml.eos_token_id", "u32", 2)]
+    return write_gguf(meta, tensors)
+
+
+def tiny_model(n_layer: int, neox: bool):
+    """The fixture loaded as a whole model: (Config, layer dicts for GpuLayers, head,
+    embedding Matrix)."""
+    cfg, layers, head, embd, _ = load_stage(tiny_model_file(n_layer, neox), 0, n_layer, True, True)
     return cfg, layers, head, embd
 
 
