@@ -1245,6 +1245,38 @@ __global__ __launch_bounds__(256) void vt_pack(const f16* __restrict__ vc, f16* 
     }
 }
 
+// The softmax of a 16-slot tile over a 64-entry block (block_step's): scores in log2 units
+// -> the P^T operands pb (f16) and the tile's new max and sum; corr is the factor its O takes
+// before the block's PV.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <int NDT>
+__device__ __forceinline__ void tile_softmax(State<NDT>& s, const f32x4 (&x)[4], half8 (&pb)[2], float& corr) {
+    float mx = fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3]));
+#pragma unroll
+    for (int kt = 1; kt < 4; kt++) mx = fmaxf(mx, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
+    mx = tile_max(mx);
+    float mn, ms;
+    lazy_max(s.m, mx, mn, ms, corr);
+    // P in f16 once: the block sum (dot2 chain over the pairs, tiles in order, then across
+    // lanes) and the PV operand (keys 32kc + 4g + 0..3, then 32kc + 16 + 4g + 0..3).
+    uint32_t hp[4][2];
+    float ls = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const half2 h = half2{(f16)exp2_hw(x[kt][2 * j] - ms), (f16)exp2_hw(x[kt][2 * j + 1] - ms)};
+            ls = pair_sum(h, ls);
+            hp[kt][j] = __builtin_bit_cast(uint32_t, h);
+        }
+    const float ps = tile_sum(ls);
+    s.l = s.l * corr + ps;
+    s.m = mn;
+#pragma unroll
+    for (int kc = 0; kc < 2; kc++)
+        pb[kc] = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
+}
+
 // The prefill kernel proper: one 16-slot tile per wave, W waves sharing each K and V block
 // in LDS, block_step's arithmetic per slot. Blocks stream through a ring of three LDS
 // stages (one LDS object each, K then V), one chunk's worth, fetched two blocks ahead by
@@ -1407,37 +1439,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
 #pragma unroll
     for (int c = 0; c < NKC; c++) qb[c] = q_scaled(qraw[c][0], qraw[c][1], p.sc);
 
-    // The softmax of the tile over a block (block_step's): scores in log2 units -> the P^T
-    // operands pb (f16) and the tile's new max and sum; corr is the factor its O takes
-    // before the block's PV.
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    auto softmax = [&](State<NDT>& s, const f32x4 (&x)[4], half8 (&pb)[2], float& corr) {
-        float mx = fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3]));
-#pragma unroll
-        for (int kt = 1; kt < 4; kt++)
-            mx = fmaxf(mx, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
-        mx = tile_max(mx);
-        float mn, ms;
-        lazy_max(s.m, mx, mn, ms, corr);
-        // P in f16 once: the block sum (dot2 chain over the pairs, tiles in order, then across
-        // lanes) and the PV operand (keys 32kc + 4g + 0..3, then 32kc + 16 + 4g + 0..3).
-        uint32_t hp[4][2];
-        float ls = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const half2 h = half2{(f16)exp2_hw(x[kt][2 * j] - ms), (f16)exp2_hw(x[kt][2 * j + 1] - ms)};
-                ls = pair_sum(h, ls);
-                hp[kt][j] = __builtin_bit_cast(uint32_t, h);
-            }
-        const float ps = tile_sum(ls);
-        s.l = s.l * corr + ps;
-        s.m = mn;
-#pragma unroll
-        for (int kc = 0; kc < 2; kc++)
-            pb[kc] = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
-    };
     // One block in stage S: scores, mask, softmax, PV.
     auto iter = [&](uint32_t key0, auto S) -> bool {
         constexpr int s0 = decltype(S)::value;
@@ -1472,7 +1473,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         }
         half8 pb[2];
         float corr;
-        softmax(cs, sc, pb, corr);
+        tile_softmax(cs, sc, pb, corr);
         rescale(cs.o, corr);
         // PV of the block.
         const f16* vls = ring(S) + BLK * HD;
@@ -1526,6 +1527,274 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     for (int dt = 0; dt < NDT; dt++) {
         const uint32_t d = 16 * dt + 4 * g;
         *(float4*)(o + d) = float4{R.o[dt][0] / R.l, R.o[dt][1] / R.l, R.o[dt][2] / R.l, R.o[dt][3] / R.l};
+    }
+}
+
+// The softmax of a 16-slot tile over a 64-entry block from relative scores: y = s - m, the
+// slot's running max already subtracted by the score MFMAs (their accumulators start at -m),
+// except in a list's first block (first: y = s, and the block's max becomes m). The running
+// max moves only when a block's relative max passes LAZY, and the subtraction of a new max
+// runs only in a wave where some slot's max moved. P = 2^y rounded to f16, its block sum
+// by the dot2 chain as in tile_softmax; corr is the factor O and l take (1 when m held).
+template <int NDT>
+__device__ __forceinline__ void tile_softmax_rel(State<NDT>& s, f32x4 (&y)[4], half8 (&pb)[2], float& corr,
+                                                 bool first) {
+    float my = fmaxf(fmaxf(y[0][0], y[0][1]), fmaxf(y[0][2], y[0][3]));
+#pragma unroll
+    for (int kt = 1; kt < 4; kt++) my = fmaxf(my, fmaxf(fmaxf(y[kt][0], y[kt][1]), fmaxf(y[kt][2], y[kt][3])));
+    my = tile_max(my);
+    float ms;
+    bool up;
+    if (first) {
+        ms = (my == -INFINITY) ? 0.0f : my;
+        up = true;
+        corr = 1.0f;  // O and l are still zero
+        s.m = my;
+    } else {
+        up = my > LAZY;
+        ms = up ? my : 0.0f;
+        corr = up ? exp2_hw(-my) : 1.0f;
+        s.m = up ? s.m + my : s.m;
+    }
+    if (__any(up)) {
+        keep_branch();
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[kt][i] = y[kt][i] - ms;
+    }
+    uint32_t hp[4][2];
+    float ls = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const half2 h = half2{(f16)exp2_hw(y[kt][2 * j]), (f16)exp2_hw(y[kt][2 * j + 1])};
+            ls = pair_sum(h, ls);
+            hp[kt][j] = __builtin_bit_cast(uint32_t, h);
+        }
+    const float ps = tile_sum(ls);
+    s.l = s.l * corr + ps;
+#pragma unroll
+    for (int kc = 0; kc < 2; kc++)
+        pb[kc] = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
+}
+
+// Wide line passes (prefill) on f16 caches at hd 128: every row's list in one online softmax
+// over 64-entry blocks from slot 0, one accumulator a slot (no chunk fold). Each wave takes
+// two 16-slot tiles (32 query slots), so every K and V operand read from LDS feeds two
+// MFMAs; a workgroup is four waves (128 slots: rows x the G heads of one KV head), and K and
+// V^T blocks stream HBM -> LDS by direct-to-LDS loads through a ring of two stages (32 KB
+// each), one block ahead. At 64 KB of LDS and at most 256 registers a lane, two workgroups
+// share a CU, one wave of each on every SIMD; the two are not synchronised with each other,
+// so one's softmax runs beside the other's MFMAs.
+// The arithmetic per slot is block_step's (scores by 16x16x32 f16 MFMAs in log2 units, the
+// lazy running max, P rounded to f16 once, PV into the same accumulator); a row's bits
+// depend only on its q and its list, never on the rows beside it.
+template <bool VT>
+__global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
+    constexpr int HD = 128;
+    constexpr int NKC = HD / 32, NDT = HD / 16, W = 4, NT = 2;
+    constexpr int RPI = 64 / PF_CPR;            // cache rows per load instruction
+    constexpr int LPW = BLK / RPI / W;          // load instructions per wave per block (K or V)
+    constexpr int SZ = 2 * BLK * HD;            // f16 per stage: K rows, then V (or V^T)
+    static_assert(LPW * RPI * W == BLK, "a block's rows divide over the waves");
+    __shared__ __attribute__((aligned(16))) f16 ring0[SZ];
+    __shared__ __attribute__((aligned(16))) f16 ring1[SZ];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t kvh = blockIdx.x % p.nkv;
+    const uint32_t rbi = p.nrb - 1u - blockIdx.x / p.nkv;  // heavy row blocks first
+    const uint32_t r0 = rbi * p.rb;
+    const uint32_t rlast = min(r0 + p.rb, p.rows) - 1u;
+    const uint32_t maxlen = p.pos + rlast + 1u;
+    const uint32_t kvd = p.nkv * HD;
+
+    // Slot n of tile t of this wave is slot 32w + 16t + n of the workgroup: head gh, row
+    // r0 + rl. Its Q is loaded here and converted once the first block's loads are out.
+    half8 qb[NT][NKC];
+    float4 qraw[NT][NKC][2];
+    uint32_t len[NT], orow[NT], ohead[NT];
+    bool valid[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const uint32_t sl = 32 * w + 16 * t + n;
+        const uint32_t gh = sl / p.rb, rl = sl % p.rb, r = r0 + rl;
+        valid[t] = gh < p.G && r < p.rows;
+        len[t] = valid[t] ? p.pos + r + 1u : maxlen;  // a slot with no row: zero q, no mask
+        orow[t] = r;
+        ohead[t] = kvh * p.G + gh;
+        const float* qrow = valid[t] ? p.q + ((size_t)r * p.nh + ohead[t]) * HD : (const float*)p.zero;
+#pragma unroll
+        for (int c = 0; c < NKC; c++) {
+            const float* src = valid[t] ? qrow + 32 * c + 8 * g : qrow;
+            qraw[t][c][0] = *(const float4*)src;
+            qraw[t][c][1] = *(const float4*)(src + 4);
+        }
+    }
+
+    const f16* zp = (const f16*)p.zero;
+    const f16* kcb = (const f16*)p.kc + (size_t)kvh * HD;
+    const f16* vcb = VT ? (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad : (const f16*)p.vc + (size_t)kvh * HD;
+    uint32_t krow[LPW], koff[LPW], voff[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const uint32_t q = i * W + w, row = q * RPI + lane / PF_CPR, pch = lane % PF_CPR;
+        krow[i] = row;
+        koff[i] = row * kvd + 8 * (pch ^ pf_kswz(row));
+        if constexpr (VT) {
+            const uint32_t d = q * 8 + lane / 8;
+            voff[i] = d * p.vt_npad + 8 * ((lane % 8) ^ (d % 8));
+        } else {
+            voff[i] = row * kvd + 8 * (pch ^ pf_vswz(row));
+        }
+    }
+    typedef __attribute__((address_space(3))) void lds_t;
+    auto load_block = [&](uint32_t key0, f16* kl) {
+        f16* vl = kl + BLK * HD;
+        const f16* kb = kcb + (size_t)key0 * kvd;
+        const f16* vb = VT ? vcb + key0 : vcb + (size_t)key0 * kvd;
+        if (key0 + BLK <= maxlen) {
+#pragma unroll
+            for (int i = 0; i < LPW; i++) {
+                const uint32_t q = i * W + w;
+                __builtin_amdgcn_global_load_lds((const void*)(kb + koff[i]), (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(vb + voff[i]), (lds_t*)&vl[q * (VT ? 8 * BLK : RPI * HD)], 16, 0, 0);
+            }
+        } else {
+            // The list's last block: rows past it read the zero page (the packed V^T holds
+            // zeros there already).
+#pragma unroll
+            for (int i = 0; i < LPW; i++) {
+                const uint32_t q = i * W + w;
+                const bool ok = key0 + krow[i] < maxlen;
+                const f16* ks = ok ? kb + koff[i] : zp + 8 * (lane % PF_CPR);
+                const f16* vs = (VT || ok) ? vb + voff[i] : zp + 8 * (lane % PF_CPR);
+                __builtin_amdgcn_global_load_lds((const void*)ks, (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)vs, (lds_t*)&vl[q * (VT ? 8 * BLK : RPI * HD)], 16, 0, 0);
+            }
+        }
+    };
+    uint32_t kbase[NKC], vbase[2];
+#pragma unroll
+    for (int c = 0; c < NKC; c++) kbase[c] = n * HD + 8 * ((4 * c + g) ^ n);
+#pragma unroll
+    for (int kc = 0; kc < 2; kc++) vbase[kc] = n * BLK + 8 * ((4 * kc + g) ^ (n % 8));
+    auto barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    State<NDT> st[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) state_clear(st[t]);
+    load_block(0, ring0);
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int c = 0; c < NKC; c++) qb[t][c] = q_scaled(qraw[t][c][0], qraw[t][c][1], p.sc);
+
+    // One block in stage kl: its loads in (own: the wait; everyone's: the barrier, after which
+    // no wave still reads the other stage), the next block's loads out, then scores, mask,
+    // softmax and PV of both tiles.
+    auto iter = [&](uint32_t key0, const f16* kls, f16* nxt) {
+        wait_vm<0>();
+        barrier();
+        if (key0 + BLK < maxlen) load_block(key0 + BLK, nxt);
+        // Operands are read from LDS one step ahead of the MFMAs that take them: the K tiles of
+        // hd chunk c+1 while chunk c's MFMAs run, the V^T operands of the first key half
+        // while the softmax runs, the second half's while the first half's MFMAs run.
+        auto kop = [&](int kt, int c) { return *(const half8*)&kls[kbase[c] + kt * 16 * HD]; };
+        const f16* vls = kls + BLK * HD;
+        auto vop = [&](int dt, int kc) -> half8 {
+            if constexpr (VT) {
+                return *(const half8*)&vls[vbase[kc] + dt * 16 * BLK];
+            } else {
+                const uint32_t r = 32 * kc + 4 * g + (n >> 2), ch = 2 * dt + ((n & 3) >> 1), h = n & 1;
+                const half4 lo = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
+                const uint32_t r2 = r + 16;
+                const half4 hi = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
+                return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+        };
+        // Scores relative to each slot's running max: the accumulators start at -m (at 0 in
+        // the list's first block, where m is not yet set).
+        const bool first = key0 == 0;
+        f32x4 sc[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float nm = first ? 0.0f : -st[t].m;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) sc[t][kt] = f32x4{nm, nm, nm, nm};
+        }
+        half8 ka[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) ka[kt] = kop(kt, 0);
+#pragma unroll
+        for (int c = 0; c < NKC; c++) {
+            half8 kn[4];
+            if (c + 1 < NKC) {
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++) kn[kt] = kop(kt, c + 1);
+            }
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) sc[t][kt] = mfma16(ka[kt], qb[t][c], sc[t][kt]);
+            if (c + 1 < NKC) {
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++) ka[kt] = kn[kt];
+            }
+        }
+        half8 va[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) va[dt] = vop(dt, 0);
+        half8 pb[NT][2];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (!__all(key0 + BLK <= len[t])) {
+                keep_branch();
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (key0 + 16 * kt + 4 * g + i >= len[t]) sc[t][kt][i] = -INFINITY;
+            }
+            float corr;
+            tile_softmax_rel(st[t], sc[t], pb[t], corr, first);
+            rescale(st[t].o, corr);
+        }
+        half8 vb[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) vb[dt] = vop(dt, 1);
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int t = 0; t < NT; t++) st[t].o[dt] = mfma16(va[dt], pb[t][0], st[t].o[dt]);
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int t = 0; t < NT; t++) st[t].o[dt] = mfma16(vb[dt], pb[t][1], st[t].o[dt]);
+    };
+    for (uint32_t key0 = 0;; key0 += 2 * BLK) {
+        iter(key0, ring0, ring1);
+        if (key0 + BLK >= maxlen) break;
+        iter(key0 + BLK, ring1, ring0);
+        if (key0 + 2 * BLK >= maxlen) break;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        if (!valid[t]) continue;
+        float* o = p.out + ((size_t)orow[t] * p.nh + ohead[t]) * HD;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const uint32_t d = 16 * dt + 4 * g;
+            *(float4*)(o + d) = float4{st[t].o[dt][0] / st[t].l, st[t].o[dt][1] / st[t].l, st[t].o[dt][2] / st[t].l,
+                                       st[t].o[dt][3] / st[t].l};
+        }
     }
 }
 
@@ -1806,7 +2075,9 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
                                (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, sp.vt_npad);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
-            hipExtLaunchKernelGGL((attn_prefill<8, true>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
+            hipExtLaunchKernelGGL((attn_line<true>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
+        } else if (wide && !sp.split) {
+            hipExtLaunchKernelGGL((attn_line<false>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else if (wide) {
             hipExtLaunchKernelGGL((attn_prefill<8, false>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else {

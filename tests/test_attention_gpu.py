@@ -202,10 +202,12 @@ def test_batch_invariance_and_determinism(ctx):
 
 
 def test_split_and_unsplit_give_the_same_bits(ctx):
-    """8 verify rows at a long context split across CUs by chunk; the same rows inside a
-    large batch are folded in one workgroup: identical bits (the chunk fold is fixed). And
-    every row of the large batch against passes of 200 rows, which take the other prefill
-    kernel (V read by transposing LDS reads, split by chunk)."""
+    """8 verify rows at a long context, split across CUs by chunk, against the same rows in
+    passes of 200 (too few workgroups to run unsplit: the transposing-read kernel, split by
+    chunk, combined): identical bits, the chunk fold being fixed. Every row of a large pass
+    (enough workgroups for the wide kernel: one online softmax over each row's whole list)
+    against those passes: within 1e-4, the reference's bound for a batch row against a
+    one-token pass (model.rs:641-642)."""
     nh, nkv, hd = 32, 8, 128
     pos = 3000
     big = 2100  # 8 kv heads x 66 row blocks of 32: enough workgroups to run unsplit
@@ -214,15 +216,16 @@ def test_split_and_unsplit_give_the_same_bits(ctx):
     kc, vc = rand((n, nkv * hd), 16), rand((n, nkv * hd), 17)
     a = Attn(ctx, kc, vc, bchip.F16, nh, nkv, hd)
     whole = a.run(q, big, pos, 0.0884)
-    for r0 in (0, 1000, 2092):
-        part = a.run(q[r0:r0 + 8], 8, pos + r0, 0.0884)
-        np.testing.assert_array_equal(part, whole[r0:r0 + 8], err_msg=f"rows {r0}..")
-    # Every row of the big pass (the packed-V^T kernel) against passes of 200 rows (too few
-    # workgroups to run unsplit: the transposing-read kernel, split by chunk, combined).
+    worst = 0.0
     for r0 in range(0, big, 200):
         n = min(200, big - r0)
         part = a.run(q[r0:r0 + n], n, pos + r0, 0.0884)
-        np.testing.assert_array_equal(part, whole[r0:r0 + n], err_msg=f"rows {r0}.. in a pass of {n}")
+        for v0 in (r0, r0 + n - 8):
+            verify = a.run(q[v0:v0 + 8], 8, pos + v0, 0.0884)
+            np.testing.assert_array_equal(verify, part[v0 - r0:v0 - r0 + 8], err_msg=f"rows {v0}.. in a pass of {n}")
+        worst = max(worst, float(np.abs(part - whole[r0:r0 + n]).max()))
+    print(f"wide pass against passes of 200: max abs {worst:.3g}", flush=True)
+    assert worst < 1e-4
     a.free()
 
 

@@ -4,8 +4,11 @@ against the CPU oracle (bc-infer's attention, crates/bc-infer/src/model.rs:448-4
 The oracle is a single-thread restatement, so the big passes are checked on sampled rows
 (the first, middle and last rows of a prefill; the first, middle and last steps of the verify
 loop; every sequence of the ragged batch in full) and, in full, through properties the
-reference's tests demand bit for bit: a split pass gives the bits of the whole one
-(model.rs:646), and one sequence of a ragged batch the bits of the sequence alone.
+reference's tests demand: the last rows of a prefill recomputed as a speculative verify agree
+within LINE_TOL (the reference's bound for a batch row against a one-token pass, model.rs:642;
+the wide prefill takes one online softmax over a row's whole list, the verify pass folds
+192-entry chunks, so the two round differently), and one sequence of a ragged batch gives the
+bits of the sequence alone.
 
 Gate (north star): max abs error <= 5e-3 and cosine >= 0.9999 against the f32 oracle, both
 on the f16-rounded cache (the kernel's error) and on the unrounded f32 values (total)."""
@@ -21,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 MAX_ABS = 5e-3
 MIN_COS = 0.9999
+LINE_TOL = 1e-4
 
 
 @pytest.fixture(scope="module")
@@ -60,7 +64,8 @@ def check_rows(got, q, kc, vc, r0, r1, nh, nkv, hd, scale, what):
 
 def causal_prefill(ctx, S, nh, nkv, hd, seed):
     """One layer's causal prefill of S tokens from position 0 (f16 cache), checked on sampled
-    rows against the oracle and its last 8 rows against an 8-row verify pass, bit for bit."""
+    rows against the oracle and its last 8 rows against an 8-row verify pass (within
+    LINE_TOL)."""
     say(f"prefill S={S} heads {nh}/{nkv} hd {hd}")
     q = rand((S, nh, hd), seed)
     kc, vc = rand((S, nkv * hd), seed + 1), rand((S, nkv * hd), seed + 2)
@@ -75,7 +80,9 @@ def causal_prefill(ctx, S, nh, nkv, hd, seed):
     # The last rows again as a speculative verify (8 rows at S-8: split over CUs by chunk).
     q8, o8 = ctx.upload(q[S - 8:]), ctx.zeros(8 * nh * hd * 4)
     ctx.attention(q8, kb, vb, bchip.F16, o8, None, False, 8, nh, nkv, hd, S - 8, scale)
-    np.testing.assert_array_equal(ctx.read(o8, (8, nh, hd)), got[S - 8:], err_msg=f"S={S}: verify of the last rows")
+    d = float(np.abs(ctx.read(o8, (8, nh, hd)) - got[S - 8:]).max())
+    say(f"S={S}: verify of the last rows against the prefill: max abs {d:.3g}")
+    assert d < LINE_TOL, f"S={S}: verify of the last rows differs by {d}"
     for b in (kb, vb, qb, ob, q8, o8):
         b.free()
 
