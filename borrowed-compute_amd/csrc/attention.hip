@@ -1591,10 +1591,10 @@ __device__ __forceinline__ void tile_softmax_rel(State<NDT>& s, f32x4 (&y)[4], h
 // The arithmetic per slot is block_step's (scores by 16x16x32 f16 MFMAs in log2 units, the
 // lazy running max, P rounded to f16 once, PV into the same accumulator); a row's bits
 // depend only on its q and its list, never on the rows beside it.
-template <bool VT>
+template <bool VT, int NT>
 __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
     constexpr int HD = 128;
-    constexpr int NKC = HD / 32, NDT = HD / 16, W = 4, NT = 2;
+    constexpr int NKC = HD / 32, NDT = HD / 16, W = 4;
     constexpr int RPI = 64 / PF_CPR;            // cache rows per load instruction
     constexpr int LPW = BLK / RPI / W;          // load instructions per wave per block (K or V)
     constexpr int SZ = 2 * BLK * HD;            // f16 per stage: K rows, then V (or V^T)
@@ -1620,7 +1620,7 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
     bool valid[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        const uint32_t sl = 32 * w + 16 * t + n;
+        const uint32_t sl = 16 * NT * w + 16 * t + n;
         const uint32_t gh = sl / p.rb, rl = sl % p.rb, r = r0 + rl;
         valid[t] = gh < p.G && r < p.rows;
         len[t] = valid[t] ? p.pos + r + 1u : maxlen;  // a slot with no row: zero q, no mask
@@ -2064,20 +2064,29 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     if (a.kv_type == 1 && a.hd == 128) {
         // Many rows re-read every V block many times: transpose V once (a pass over V) so
         // that its operands are plain LDS reads. The result is the same bits either way.
-        const bool use_vt = wide && !sp.split && a.rows >= 256;
-        if (use_vt) {
-            const uint32_t nb = ceil_div(maxlen, 64);
-            sp.vt_npad = nb * 64;
-            e = ws.reserve_vt((size_t)a.nkv * 128 * sp.vt_npad * 2);
-            if (e != hipSuccess) return e;
-            sp.vt = ws.vt;
-            hipLaunchKernelGGL(vt_pack, dim3(nb, a.nkv), dim3(256), 0, s, (const f16*)a.vc,
-                               (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, sp.vt_npad);
-            e = hipGetLastError();
-            if (e != hipSuccess) return e;
-            hipExtLaunchKernelGGL((attn_line<true>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
-        } else if (wide && !sp.split) {
-            hipExtLaunchKernelGGL((attn_line<false>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
+        // Measured: the pass pays from about 3000 rows (4096 rows of 64/8 heads: 323 against
+        // 330 us a call; 2048 rows of 32/8: 73 against 69 us).
+        const bool use_vt = wide && !sp.split && a.rows >= 3072;
+        if (wide && !sp.split) {
+            // The wide kernel, two 16-slot tiles a wave, four waves: 128 slots a workgroup as
+            // sp.rb is sized. (One tile a wave, 64 slots a workgroup, measured the same at
+            // 2048 rows: 62.7 against 62.2 us; there the heaviest row block's chain of blocks,
+            // each about 1.9 us of latency, bounds the pass.)
+            SharedParams lp = sp;
+            if (use_vt) {
+                const uint32_t nb = ceil_div(maxlen, 64);
+                lp.vt_npad = nb * 64;
+                e = ws.reserve_vt((size_t)a.nkv * 128 * lp.vt_npad * 2);
+                if (e != hipSuccess) return e;
+                lp.vt = ws.vt;
+                hipLaunchKernelGGL(vt_pack, dim3(nb, a.nkv), dim3(256), 0, s, (const f16*)a.vc,
+                                   (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, lp.vt_npad);
+                e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                hipExtLaunchKernelGGL((attn_line<true, 2>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, lp);
+            } else {
+                hipExtLaunchKernelGGL((attn_line<false, 2>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, lp);
+            }
         } else if (wide) {
             hipExtLaunchKernelGGL((attn_prefill<8, false>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else {
