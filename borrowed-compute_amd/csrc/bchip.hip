@@ -42,6 +42,7 @@ struct bchip_ctx {
     hipEvent_t t0 = nullptr, t1 = nullptr;
     Workspace ws;
     Workspace fixed_ws;  // the scratch array's device copy, for the no-allocation entry point
+    uint32_t* mm_cnt = nullptr;  // the batched products' arrival counters (MATMUL_COUNTERS, zero between calls)
     std::map<uintptr_t, size_t> allocs;  // base -> bytes, of bchip_alloc memory
     std::string name;
     hipEvent_t arm_before = nullptr, arm_after = nullptr;  // bchip_timer_arm, for the next call
@@ -250,6 +251,8 @@ int bchip_init(int device, bchip_ctx** out) {
         e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
         if (e == hipSuccess) c->fixed_ws.set_fixed(sp, NOALLOC_O_BYTES, NOALLOC_ML_BYTES, NOALLOC_Q_BYTES, c->ws.zero);
     }
+    if (e == hipSuccess) e = hipMalloc((void**)&c->mm_cnt, MATMUL_COUNTERS * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c->mm_cnt, 0, MATMUL_COUNTERS * sizeof(uint32_t));
     if (e == hipSuccess) e = hipEventCreate(&c->t0);
     if (e == hipSuccess) e = hipEventCreate(&c->t1);
     if (e != hipSuccess) {
@@ -266,6 +269,7 @@ int bchip_destroy(bchip_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     c->ws.release();
     if (c->ws.zero) (void)hipFree(c->ws.zero);
+    if (c->mm_cnt) (void)hipFree(c->mm_cnt);
     for (auto& a : c->allocs) (void)hipFree((void*)a.first);
     if (c->t0) (void)hipEventDestroy(c->t0);
     if (c->t1) (void)hipEventDestroy(c->t1);
@@ -387,7 +391,13 @@ int bchip_matmul(bchip_ctx* c, const void* w, uint32_t type, const float* x, flo
     CHECK(check_span(c, w, row_bytes * rows, "weights"));
     CHECK(check_span(c, x, (uint64_t)n * cols * 4, "x"));
     CHECK(check_span(c, out, (uint64_t)n * rows * 4, "out"));
-    HIP_TRY(matmul_launch(w, type, x, out, rows, cols, n, (uint32_t)row_bytes, c->stream), "matmul");
+    void* scratch = nullptr;
+    if (const size_t sb = matmul_scratch_bytes(type, rows, cols, n)) {
+        HIP_TRY(c->ws.reserve_vt(sb), "matmul scratch");
+        scratch = c->ws.vt;
+    }
+    HIP_TRY(matmul_launch(w, type, x, out, rows, cols, n, (uint32_t)row_bytes, scratch, c->mm_cnt, c->stream),
+            "matmul");
     return BCHIP_OK;
 }
 

@@ -111,8 +111,14 @@ hipError_t sample_launch(const float* scores, uint32_t rows, uint32_t vocab, flo
 bool ggml_block(uint32_t type, uint32_t& weights, uint32_t& bytes);
 // Input rows one product call takes: passes of 8 rows over the grid's y dimension (65535).
 constexpr uint32_t MATMUL_MAX_N = 8u * 65535u;
+// Batches of n >= 8 input rows of the quantised formats and F16 (cols a multiple of 256)
+// run on the matrix cores; their K splits may need matmul_scratch_bytes of scratch (partial
+// sums) and a context's MATMUL_COUNTERS arrival counters (zero when no product runs).
+constexpr uint32_t MATMUL_COUNTERS = 1024;
+bool matmul_uses_mm(uint32_t type, uint32_t cols, uint32_t n);
+size_t matmul_scratch_bytes(uint32_t type, uint32_t rows, uint32_t cols, uint32_t n);
 hipError_t matmul_launch(const void* w, uint32_t type, const float* x, float* out, uint32_t rows, uint32_t cols,
-                         uint32_t n, uint32_t row_bytes, hipStream_t s);
+                         uint32_t n, uint32_t row_bytes, void* scratch, uint32_t* counters, hipStream_t s);
 hipError_t rms_norm_launch(const float* x, const float* w, float* out, uint32_t rows, uint32_t cols, float eps,
                            bool vec, hipStream_t s);
 enum : int { EW_BIAS = 0, EW_SILU_MUL = 1, EW_ADD = 2 };

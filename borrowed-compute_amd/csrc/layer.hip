@@ -350,6 +350,474 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_matmul(const MatmulParams p) 
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Batched product on the matrix cores (n >= MM_MIN input rows; the reference switches its
+// batches to a matrix-unit product the same way, gpu/mod.rs:33-41, metal.rs:153-197).
+// In the affine form, group g of weight row r is w = a q + b, q a small integer (exact in
+// f16); where b is a fixed multiple of a (Q4_0, Q5_0, Q8_0, Q6K) the offset is folded into
+// q, so sum_k w x = a sum q x (+ b sum x for Q4_1, Q5_1, Q4K, Q5K). The MFMAs compute
+// sum q x with x split into f16 parts, x = hi + lo 2^-12 (lo stored scaled by 2^12, so it
+// stays a normal f16; hi is zero where it would be subnormal): about 22 bits, each product
+// exact in f32, f32-level sums.
+//
+// k_matmul_mm: a workgroup is four waves of 16 weight rows (64 rows), eight input rows and
+// a K range of at most MMK units of 256 columns. The range's x is staged once in LDS as 16
+// A rows: rows 0..7 the eight inputs' hi, rows 8..15 their lo, so one v_mfma_f32_16x16x32
+// _f16 over group g gives D[i][l] = sum hi_i q (i < 8) and sum lo_{i-8} q (i >= 8) for the
+// wave's 16 rows at once. Lane 16 c + l holds weights 8c .. 8c + 7 of group g of row r0 + l
+// as its B operand, unpacked from the ggml bytes in registers (bytes to f16 by v_perm_b32
+// onto 1024 + v, then one packed f16 subtraction that also removes the format's offset),
+// and D[4c + i][l]: c < 2 the hi sums of input 4c + i, c >= 2 the lo sums of input
+// 4(c - 2) + i. Per group each lane adds a_eff D[i] (a_eff = a, or a 2^-12 in lo lanes) and
+// b s[i] (s the group's sum of x, zero for lo lanes) to its four accumulators; the hi and
+// lo accumulators meet once at the end. The units' bytes are loaded MM_PF units ahead. Q6K
+// (a scale a 16 weights) takes two v_mfma_f32_16x16x16_f16 a group, one a half; F16 has
+// no scale and chains its MFMAs through the accumulators. K splits: their number depends
+// on rows and cols only; a split's partial is hi + lo of its units in order, and the row's
+// result the splits' partials added in split order, whether one workgroup runs the splits
+// one after another or ks workgroups run them at once and the last to finish (a device
+// counter per tile) adds them: an input row's bits depend on that row alone, never on n
+// or its place in the batch.
+constexpr float MM_LO = 4096.0f;   // lo = (x - hi) * MM_LO
+constexpr uint32_t MM_MIN = 8;     // batches of at least this many rows take the matrix cores
+constexpr uint32_t MMK = 8;        // units (256 columns) a K split at most
+constexpr uint32_t MM_XS = MMK * 256 + 8;  // LDS halves a staged x row: 16-byte reads of 16 rows on distinct banks
+constexpr uint32_t MM_PAR = MATMUL_COUNTERS;  // tiles (64 rows x 8 inputs) up to which K splits run in parallel
+
+template <uint32_t TY>
+constexpr bool mm_type() {
+    return TY == G_F16 || TY == G_Q8_0 || TY == G_Q4_0 || TY == G_Q4_1 || TY == G_Q5_0 || TY == G_Q5_1 ||
+           TY == G_Q4K || TY == G_Q5K || TY == G_Q6K;
+}
+// Formats with a per-group b not a multiple of a: the product adds b sum x.
+template <uint32_t TY>
+constexpr bool mm_sum() {
+    return TY == G_Q4_1 || TY == G_Q5_1 || TY == G_Q4K || TY == G_Q5K;
+}
+// Dwords a lane holds of one unit (8 groups) of its row.
+template <uint32_t TY>
+constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 32 : TY == G_Q4_0 ? 32 : TY == G_Q4_1 ? 24
+                 : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 14 : 32;
+// Units loaded ahead.
+template <uint32_t TY>
+constexpr int MM_PF = MW<TY> <= 16 ? 3 : 2;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Bytes 0..3 of v, each 1024 + v_k - off exact in f16 (v_k < 256, off an f16 integer):
+// two f16 pairs.
+__device__ __forceinline__ u32x2 bytes_f16(uint32_t v, half2 off) {
+    const uint32_t e0 = __builtin_amdgcn_perm(0x64646464u, v, 0x05010400u);  // (b0 | 0x6400, b1 | 0x6400)
+    const uint32_t e1 = __builtin_amdgcn_perm(0x64646464u, v, 0x05030402u);  // (b2 | 0x6400, b3 | 0x6400)
+    const half2 h0 = __builtin_bit_cast(half2, e0) - off, h1 = __builtin_bit_cast(half2, e1) - off;
+    return u32x2{__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
+}
+// Eight byte values (two dwords) as a B operand.
+__device__ __forceinline__ half8 bytes8_f16(uint32_t v0, uint32_t v1, half2 off) {
+    const u32x2 a = bytes_f16(v0, off), b = bytes_f16(v1, off);
+    return __builtin_bit_cast(half8, u32x4{a[0], a[1], b[0], b[1]});
+}
+// Four bits to bit 4 of bytes 0..3.
+__device__ __forceinline__ uint32_t bit4_spread(uint32_t b4) { return ((b4 * 0x00204081u) & 0x01010101u) << 4; }
+// Eight bytes at a 2-byte-aligned p from the three dwords loaded at p & ~3 (`ld3`).
+__device__ __forceinline__ void ld3(const uint8_t* p, uint32_t* d) {
+    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+    d[0] = *(const uint32_t*)a;
+    d[1] = *(const uint32_t*)(a + 4);
+    // the third dword only holds bytes of p's eight when sh = 2; otherwise the second again,
+    // so that no read touches a dword past the eight bytes' last
+    d[2] = *(const uint32_t*)(a + 4 + 2 * sh);
+}
+__device__ __forceinline__ void align8(const uint8_t* p, const uint32_t* d, uint32_t& w0, uint32_t& w1) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+    w0 = __builtin_amdgcn_alignbyte(d[1], d[0], sh);
+    w1 = __builtin_amdgcn_alignbyte(d[2], d[1], sh);
+}
+
+// Lane (c, row) loads of unit u (8 groups) of its row.
+template <uint32_t TY>
+__device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_t u, uint32_t c,
+                                        uint32_t (&d)[MW<TY>]) {
+    if constexpr (TY == G_F16) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const u32x4 v = *(const u32x4*)(row + (size_t)(8 * u + j) * 64 + 16 * c);
+            d[4 * j] = v[0]; d[4 * j + 1] = v[1]; d[4 * j + 2] = v[2]; d[4 * j + 3] = v[3];
+        }
+    } else if constexpr (TY == G_Q8_0 || TY == G_Q4_0) {
+        constexpr uint32_t BS = TY == G_Q8_0 ? 34 : 18;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint8_t* bb = row + (size_t)(8 * u + j) * BS;
+            ld3(bb + 2 + (TY == G_Q8_0 ? 8 * c : 8 * (c & 1)), &d[4 * j]);
+            d[4 * j + 3] = ld16(bb);
+        }
+    } else if constexpr (TY == G_Q5_0) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint8_t* bb = row + (size_t)(8 * u + j) * 22;
+            ld3(bb + 6 + 8 * (c & 1), &d[5 * j]);
+            d[5 * j + 3] = ld16(bb);
+            d[5 * j + 4] = ld16(bb + 2 + 2 * (c >> 1));  // qh bytes 2 (c / 2), 2 (c / 2) + 1
+        }
+    } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
+        constexpr uint32_t BS = TY == G_Q4_1 ? 20 : 24, QS = TY == G_Q4_1 ? 4 : 8, N = MW<TY> / 8;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint8_t* bb = row + (size_t)(8 * u + j) * BS;
+            d[N * j] = ld32(bb + QS + 8 * (c & 1));
+            d[N * j + 1] = ld32(bb + QS + 8 * (c & 1) + 4);
+            d[N * j + 2] = ld32(bb);  // d, m
+            if constexpr (TY == G_Q5_1) d[N * j + 3] = ld32(bb + 4);  // qh
+        }
+    } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
+        constexpr uint32_t BS = TY == G_Q4K ? 144 : 176, QS = TY == G_Q4K ? 16 : 48;
+        const uint8_t* bb = row + (size_t)u * BS;
+        const u32x4 h = *(const u32x4*)bb;  // d, dmin, the 12 scale bytes
+        d[0] = h[0]; d[1] = h[1]; d[2] = h[2]; d[3] = h[3];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const u32x2 v = *(const u32x2*)(bb + QS + 32 * k + 8 * c);
+            d[4 + 2 * k] = v[0];
+            d[5 + 2 * k] = v[1];
+        }
+        if constexpr (TY == G_Q5K) {
+            const u32x2 v = *(const u32x2*)(bb + 16 + 8 * c);  // qh bytes 8c .. 8c + 7
+            d[12] = v[0];
+            d[13] = v[1];
+        }
+    } else {  // Q6K: lane c's weights 4c .. 4c + 3 and 16 + 4c .. of each 32-weight run
+        const uint8_t* bb = row + (size_t)u * 210;
+        const uintptr_t a = (uintptr_t)bb & ~(uintptr_t)3;
+        // ql runs 0..3 (64 hh + 32 s), qh runs 0..1 (128 + 32 hh): dwords at 4c and 16 + 4c of
+        // the run (two each, from the aligned base); then scales and d (bytes 192..209)
+#pragma unroll
+        for (int k = 0; k < 6; k++) {
+            const uint32_t o = k < 4 ? 32 * k : 128 + 32 * (k - 4);
+            d[4 * k] = *(const uint32_t*)(a + o + 4 * c);
+            d[4 * k + 1] = *(const uint32_t*)(a + o + 4 * c + 4);
+            d[4 * k + 2] = *(const uint32_t*)(a + o + 16 + 4 * c);
+            d[4 * k + 3] = *(const uint32_t*)(a + o + 20 + 4 * c);
+        }
+#pragma unroll
+        for (int k = 0; k < 5; k++) d[24 + k] = *(const uint32_t*)(a + 192 + 4 * k);
+    }
+}
+
+// Group j of a loaded unit for lane c: B operand(s), a (fl folded in) and b. Q6K gives two
+// half operands q4[0], q4[1] (16x16x16 MFMAs) and a0, a1.
+template <uint32_t TY>
+__device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const uint8_t* unit_base, int j, uint32_t c,
+                                         float fl, half8& q, half4 (&q4)[2], float& a0, float& a1, float& b) {
+    if constexpr (TY == G_F16) {
+        q = __builtin_bit_cast(half8, u32x4{d[4 * j], d[4 * j + 1], d[4 * j + 2], d[4 * j + 3]});
+    } else if constexpr (TY == G_Q8_0) {
+        const uint8_t* p = unit_base + 34 * j + 2 + 8 * c;
+        uint32_t w0, w1;
+        align8(p, &d[4 * j], w0, w1);
+        q = bytes8_f16(w0 ^ 0x80808080u, w1 ^ 0x80808080u, half2{(f16)1152.0f, (f16)1152.0f});
+        a0 = h2f(d[4 * j + 3]) * fl;
+    } else if constexpr (TY == G_Q4_0) {
+        const uint8_t* p = unit_base + 18 * j + 2 + 8 * (c & 1);
+        uint32_t w0, w1;
+        align8(p, &d[4 * j], w0, w1);
+        // lanes 0, 1: low nibbles, lanes 2, 3: high nibbles (weights 16 ..), as q - 8
+        const uint32_t sh = c < 2 ? 0u : 4u;
+        q = bytes8_f16((w0 >> sh) & 0x0f0f0f0fu, (w1 >> sh) & 0x0f0f0f0fu, half2{(f16)1032.0f, (f16)1032.0f});
+        a0 = h2f(d[4 * j + 3]) * fl;
+    } else if constexpr (TY == G_Q5_0) {
+        const uint8_t* p = unit_base + 22 * j + 6 + 8 * (c & 1);
+        uint32_t w0, w1;
+        align8(p, &d[5 * j], w0, w1);
+        const uint32_t sh = c < 2 ? 0u : 4u;
+        const uint32_t qh = (d[5 * j + 4] >> (8 * (c & 1))) & 255u;  // qh byte c: bit 4 of weights 8c ..
+        w0 = ((w0 >> sh) & 0x0f0f0f0fu) | bit4_spread(qh & 15u);
+        w1 = ((w1 >> sh) & 0x0f0f0f0fu) | bit4_spread(qh >> 4);
+        q = bytes8_f16(w0, w1, half2{(f16)1040.0f, (f16)1040.0f});
+        a0 = h2f(d[5 * j + 3]) * fl;
+    } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
+        constexpr uint32_t N = MW<TY> / 8;
+        uint32_t w0 = d[N * j], w1 = d[N * j + 1];
+        // lanes 0, 1: low nibbles, lanes 2, 3: high nibbles (weights 16 ..); Q5_1 adds qh byte c
+        // as bit 4. (The nibbles' scale must be the same across a group's k: the MFMA sums it.)
+        const uint32_t sh = c < 2 ? 0u : 4u;
+        w0 = (w0 >> sh) & 0x0f0f0f0fu;
+        w1 = (w1 >> sh) & 0x0f0f0f0fu;
+        if constexpr (TY == G_Q5_1) {
+            const uint32_t qh = (d[N * j + 3] >> (8 * c)) & 255u;
+            w0 |= bit4_spread(qh & 15u);
+            w1 |= bit4_spread(qh >> 4);
+        }
+        q = bytes8_f16(w0, w1, half2{(f16)1024.0f, (f16)1024.0f});
+        a0 = h2f(d[N * j + 2] & 0xffffu) * fl;
+        b = h2f(d[N * j + 2] >> 16);
+    } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
+        const int k = j / 2, hi = j % 2;
+        uint32_t w0 = d[4 + 2 * k], w1 = d[5 + 2 * k];
+        float sc16 = 1.0f;
+        if constexpr (TY == G_Q4K) {
+            const uint32_t m = hi ? 0xf0f0f0f0u : 0x0f0f0f0fu;  // high nibbles in place: 16 q
+            w0 &= m;
+            w1 &= m;
+            sc16 = hi ? 0.0625f : 1.0f;
+        } else {
+            w0 = ((w0 >> (4 * hi)) & 0x0f0f0f0fu) | (((d[12] >> j) & 0x01010101u) << 4);
+            w1 = ((w1 >> (4 * hi)) & 0x0f0f0f0fu) | (((d[13] >> j) & 0x01010101u) << 4);
+        }
+        q = bytes8_f16(w0, w1, half2{(f16)1024.0f, (f16)1024.0f});
+        // scale and min of sub-block j (6 bits each, quant.rs:136-146)
+        const uint32_t s0 = d[1], s1 = d[2], s2 = d[3];
+        uint32_t scb, mnb;
+        if (j < 4) {
+            scb = (s0 >> (8 * j)) & 63u;
+            mnb = (s1 >> (8 * j)) & 63u;
+        } else {
+            const int t = 8 * (j - 4);
+            scb = ((s2 >> t) & 15u) | (((s0 >> t) >> 2) & 0x30u);
+            mnb = ((s2 >> t) >> 4 & 15u) | (((s1 >> t) >> 2) & 0x30u);
+        }
+        const float dd = h2f(d[0] & 0xffffu), dm = h2f(d[0] >> 16);
+        a0 = dd * (float)scb * (fl * sc16);
+        b = -(dm * (float)mnb);
+    } else {  // Q6K
+        const int hh = j / 4, qr = j % 4, s = qr & 1;
+        const uint32_t sh = (uint32_t)((uintptr_t)unit_base & 3u);
+        // lane c: weights 4c .. 4c + 3 (half 0) and 16 + 4c .. (half 1) of the group
+        const uint32_t* L = &d[4 * (2 * hh + s)];
+        const uint32_t* H = &d[4 * (4 + hh)];
+        const uint32_t l0 = __builtin_amdgcn_alignbyte(L[1], L[0], sh), l1 = __builtin_amdgcn_alignbyte(L[3], L[2], sh);
+        const uint32_t h0 = __builtin_amdgcn_alignbyte(H[1], H[0], sh), h1 = __builtin_amdgcn_alignbyte(H[3], H[2], sh);
+        const uint32_t ns = qr < 2 ? 0u : 4u;
+        const uint32_t v0 = ((l0 >> ns) & 0x0f0f0f0fu) | (((h0 >> (2 * qr)) & 0x03030303u) << 4);
+        const uint32_t v1 = ((l1 >> ns) & 0x0f0f0f0fu) | (((h1 >> (2 * qr)) & 0x03030303u) << 4);
+        const half2 o = half2{(f16)1056.0f, (f16)1056.0f};
+        const u32x2 e0 = bytes_f16(v0, o), e1 = bytes_f16(v1, o);
+        q4[0] = __builtin_bit_cast(half4, e0);
+        q4[1] = __builtin_bit_cast(half4, e1);
+        // scales (int8) 8 hh + 2 qr and + 1, d: bytes 192 .. 209 of the block
+        const uint32_t sw = __builtin_amdgcn_alignbyte(d[25 + hh * 2 + (qr >> 1)], d[24 + hh * 2 + (qr >> 1)], sh);
+        const uint32_t sp = sw >> (16 * (qr & 1));  // bytes 2 qr, 2 qr + 1 of the 4-byte window
+        const uint32_t dw = __builtin_amdgcn_alignbyte(d[28], d[28], sh) & 0xffffu;  // d: bytes 208, 209
+        const float dd = h2f(dw) * fl;
+        a0 = dd * (float)(int8_t)(uint8_t)(sp & 255u);
+        a1 = dd * (float)(int8_t)(uint8_t)((sp >> 8) & 255u);
+    }
+}
+
+struct MMParams {
+    const uint8_t* w;
+    const float* x;
+    float* out;
+    float* part;    // [ks][npad][rows]: parallel splits' partials
+    uint32_t* cnt;  // [tiles]: arrivals of a tile's parallel splits (zero between calls)
+    uint32_t rows, cols, n, npad, row_bytes, units, ks, par;
+};
+
+template <uint32_t TY>
+__global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
+    constexpr bool SUM = mm_sum<TY>();
+    constexpr int PF = MM_PF<TY>;
+    constexpr uint32_t BS = TY == G_F16 ? 512 : TY == G_Q8_0 ? 272 : TY == G_Q4_0 ? 144 : TY == G_Q4_1 ? 160
+                          : TY == G_Q5_0 ? 176 : TY == G_Q5_1 ? 192 : TY == G_Q4K ? 144 : TY == G_Q5K ? 176 : 210;
+    __shared__ __attribute__((aligned(16))) f16 xs[16 * MM_XS];
+    __shared__ __attribute__((aligned(16))) float ss[SUM ? MMK * 8 * 16 : 4];
+    __shared__ uint32_t last;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t c = lane >> 4, rl = lane & 15;
+    const uint32_t r = blockIdx.x * 64 + 16 * w + rl, i0 = blockIdx.y * 8;
+    const bool live = blockIdx.x * 64 + 16 * w < p.rows;  // the wave has rows
+    const uint8_t* rowp = p.w + (size_t)min(r, p.rows - 1) * p.row_bytes;
+    const float fl = c >= 2 ? 1.0f / MM_LO : 1.0f;
+    const uint32_t kz0 = p.par ? blockIdx.z : 0, kz1 = p.par ? blockIdx.z + 1 : p.ks;
+    float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t kz = kz0; kz < kz1; kz++) {
+        const uint32_t ua = kz * p.units / p.ks, nu = (kz + 1) * p.units / p.ks - ua;
+        // Every step loads one unit (past the range's end its last unit again), so the loads
+        // outstanding at each use are the same and the compiler's waits stay partial.
+        uint32_t pk[PF][MW<TY>];
+        if (live) {
+#pragma unroll
+            for (int f = 0; f < PF; f++) mm_load<TY>(rowp, ua + min((uint32_t)f, nu - 1), c, pk[f]);
+        }
+        if (kz != kz0) __syncthreads();  // every wave is done with the previous split's x
+        // Stage x: thread pairs (input i, group g) of the range, 32 values each: hi, lo and
+        // (SUM) the group's sum in order.
+        const uint32_t ng = 8 * nu;
+        for (uint32_t e = tid; e < 8 * ng; e += 256) {
+            const uint32_t i = e / ng, g = e % ng, in = i0 + i;
+            float v[32];
+            if (in < p.n) {
+                const float4* src = (const float4*)(p.x + (size_t)in * p.cols + (size_t)ua * 256 + 32 * g);
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float4 t = src[k];
+                    v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 32; k++) v[k] = 0.0f;
+            }
+            if constexpr (SUM) {
+                float s = v[0];
+#pragma unroll
+                for (int k = 1; k < 32; k++) s += v[k];
+                ss[g * 16 + i] = s;
+                ss[g * 16 + 8 + i] = 0.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                half8 h, l;
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const float x = v[8 * k + t];
+                    f16 hv = (f16)x;
+                    if (__builtin_fabsf((float)hv) < 6.103515625e-05f) hv = (f16)0.0f;
+                    h[t] = hv;
+                    l[t] = (f16)((x - (float)hv) * MM_LO);
+                }
+                *(half8*)&xs[i * MM_XS + 32 * g + 8 * k] = h;
+                *(half8*)&xs[(8 + i) * MM_XS + 32 * g + 8 * k] = l;
+            }
+        }
+        __syncthreads();
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (live) {
+            for (uint32_t u0 = 0; u0 < nu; u0 += PF) {
+#pragma unroll
+                for (int f = 0; f < PF; f++) {
+                    const uint32_t lu = u0 + f;
+                    if (lu < nu) {
+                        const uint8_t* ub = rowp + (size_t)(ua + lu) * BS;
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const uint32_t col = lu * 256 + 32 * j;
+                            half8 q;
+                            half4 q4[2];
+                            float a0 = 0.0f, a1 = 0.0f, b = 0.0f;
+                            mm_group<TY>(pk[f], ub, j, c, fl, q, q4, a0, a1, b);
+                            if constexpr (TY == G_F16) {
+                                const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
+                                acc = mfma16(xa, q, acc);
+                            } else if constexpr (TY == G_Q6K) {
+                                const half4 x0 = *(const half4*)&xs[rl * MM_XS + col + 4 * c];
+                                const half4 x1 = *(const half4*)&xs[rl * MM_XS + col + 16 + 4 * c];
+                                const f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                                const f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x16f16(x0, q4[0], z, 0, 0, 0);
+                                const f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x16f16(x1, q4[1], z, 0, 0, 0);
+#pragma unroll
+                                for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(a1, d1[i], __builtin_fmaf(a0, d0[i], acc[i]));
+                            } else {
+                                const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
+                                const f32x4 dv = mfma16(xa, q, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                                if constexpr (SUM) {
+                                    const f32x4 s = *(const f32x4*)&ss[(lu * 8 + j) * 16 + 4 * c];
+#pragma unroll
+                                    for (int i = 0; i < 4; i++)
+                                        acc[i] = __builtin_fmaf(b, s[i], __builtin_fmaf(a0, dv[i], acc[i]));
+                                } else {
+#pragma unroll
+                                    for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(a0, dv[i], acc[i]);
+                                }
+                            }
+                        }
+                    }
+                    // the unit's registers are free: load into them directly (a load hoisted
+                    // above their last use would land in other registers and wait to be copied)
+                    __builtin_amdgcn_sched_barrier(0);
+                    mm_load<TY>(rowp, ua + min(lu + PF, nu - 1), c, pk[f]);
+                }
+            }
+        }
+        if constexpr (TY == G_F16) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] *= fl;
+        }
+        // the split's partial: hi + lo, in lanes c < 2 (input 4c + i); then splits in order
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float pt = acc[i] + __shfl_xor(acc[i], 32, 64);
+            tot[i] = kz == kz0 ? pt : tot[i] + pt;
+        }
+    }
+    if (!p.par) {
+        if (c < 2 && r < p.rows) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (i0 + 4 * c + i < p.n) p.out[(size_t)(i0 + 4 * c + i) * p.rows + r] = tot[i];
+        }
+        return;
+    }
+    // Parallel splits: the partial to device memory (write-through stores), then the tile's
+    // arrival count; the last workgroup of the tile adds the partials in split order.
+    if (c < 2 && r < p.rows) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __hip_atomic_store(&p.part[((size_t)blockIdx.z * p.npad + i0 + 4 * c + i) * p.rows + r], tot[i],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
+    __syncthreads();
+    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&p.cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == p.ks - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    for (uint32_t e = tid; e < 512; e += 256) {
+        const uint32_t rr = blockIdx.x * 64 + e % 64, in = i0 + e / 64;
+        if (rr < p.rows && in < p.n) {
+            const float* src = p.part + (size_t)in * p.rows + rr;
+            const size_t stride = (size_t)p.npad * p.rows;
+            float s = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t k = 1; k < p.ks; k++)
+                s += __hip_atomic_load(src + k * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            p.out[(size_t)in * p.rows + rr] = s;
+        }
+    }
+    if (tid == 0) __hip_atomic_store(&p.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// K splits of a product: about two workgroups a CU from the rows alone (never from n), each
+// split at most MMK units.
+static uint32_t mm_ks(uint32_t rows, uint32_t cols) {
+    const uint32_t rt = (rows + 63) / 64, units = cols / 256;
+    uint32_t ks = (512u + rt / 2) / rt;
+    ks = max(ks, (units + MMK - 1) / MMK);
+    ks = min(ks, units);
+    return max(ks, 1u);
+}
+static bool mm_par(uint32_t rows, uint32_t cols, uint32_t n) {
+    const uint32_t rt = (rows + 63) / 64, nt = (n + 7) / 8;
+    return mm_ks(rows, cols) > 1 && (uint64_t)rt * nt <= MM_PAR;
+}
+
+bool matmul_uses_mm(uint32_t type, uint32_t cols, uint32_t n) {
+    switch (type) {
+        case G_F16: case G_Q8_0: case G_Q4_0: case G_Q4_1: case G_Q5_0: case G_Q5_1: case G_Q4K: case G_Q5K:
+        case G_Q6K: return n >= MM_MIN && cols % 256 == 0;
+        default: return false;
+    }
+}
+
+size_t matmul_scratch_bytes(uint32_t type, uint32_t rows, uint32_t cols, uint32_t n) {
+    if (!matmul_uses_mm(type, cols, n) || !mm_par(rows, cols, n)) return 0;
+    return (size_t)mm_ks(rows, cols) * ((n + 7) / 8 * 8) * rows * sizeof(float);
+}
+
+template <uint32_t TY>
+static hipError_t matmul_mm_go(const MatmulParams& mp, void* scratch, uint32_t* counters, hipStream_t s) {
+    const uint32_t ks = mm_ks(mp.rows, mp.cols), rt = (mp.rows + 63) / 64, nt = (mp.n + 7) / 8;
+    const bool par = mm_par(mp.rows, mp.cols, mp.n);
+    if (par && (!scratch || !counters)) return hipErrorInvalidValue;
+    const MMParams q{mp.w, mp.x, mp.out, (float*)scratch, counters, mp.rows, mp.cols, mp.n, nt * 8, mp.row_bytes,
+                     mp.cols / 256, ks, par ? 1u : 0u};
+    hipLaunchKernelGGL((k_matmul_mm<TY>), dim3(rt, nt, par ? ks : 1), dim3(256), 0, s, q);
+    return hipGetLastError();
+}
+
 template <uint32_t TY, int NBT, int R>
 static void matmul_go(const MatmulParams& mp, hipStream_t s) {
     const uint32_t per_wg = MM_WAVES * R;
@@ -362,7 +830,10 @@ static void matmul_go(const MatmulParams& mp, hipStream_t s) {
 // the matrix still gives 256+ workgroups (measured: the 14336 x 4096 Q4K product 21.3 ->
 // 14.2 µs), else four. Batches: four rows a wave, eight input rows a pass.
 template <uint32_t TY>
-static hipError_t matmul_t(const MatmulParams& mp, hipStream_t s) {
+static hipError_t matmul_t(const MatmulParams& mp, void* scratch, uint32_t* counters, hipStream_t s) {
+    if constexpr (mm_type<TY>()) {
+        if (matmul_uses_mm(TY, mp.cols, mp.n)) return matmul_mm_go<TY>(mp, scratch, counters, s);
+    }
     if (mp.n == 1) {
         if (PK<TY> <= 12 && mp.rows >= 256u * MM_WAVES * 8)
             matmul_go<TY, 1, (PK<TY> <= 12 ? 8 : 4)>(mp, s);
@@ -375,20 +846,20 @@ static hipError_t matmul_t(const MatmulParams& mp, hipStream_t s) {
 }
 
 hipError_t matmul_launch(const void* w, uint32_t type, const float* x, float* out, uint32_t rows, uint32_t cols,
-                         uint32_t n, uint32_t row_bytes, hipStream_t s) {
+                         uint32_t n, uint32_t row_bytes, void* scratch, uint32_t* counters, hipStream_t s) {
     const MatmulParams mp{(const uint8_t*)w, x, out, rows, cols, n, row_bytes};
     switch (type) {
-        case G_F32: return matmul_t<G_F32>(mp, s);
-        case G_F16: return matmul_t<G_F16>(mp, s);
-        case G_BF16: return matmul_t<G_BF16>(mp, s);
-        case G_Q4_0: return matmul_t<G_Q4_0>(mp, s);
-        case G_Q4_1: return matmul_t<G_Q4_1>(mp, s);
-        case G_Q5_0: return matmul_t<G_Q5_0>(mp, s);
-        case G_Q5_1: return matmul_t<G_Q5_1>(mp, s);
-        case G_Q8_0: return matmul_t<G_Q8_0>(mp, s);
-        case G_Q4K: return matmul_t<G_Q4K>(mp, s);
-        case G_Q5K: return matmul_t<G_Q5K>(mp, s);
-        case G_Q6K: return matmul_t<G_Q6K>(mp, s);
+        case G_F32: return matmul_t<G_F32>(mp, scratch, counters, s);
+        case G_F16: return matmul_t<G_F16>(mp, scratch, counters, s);
+        case G_BF16: return matmul_t<G_BF16>(mp, scratch, counters, s);
+        case G_Q4_0: return matmul_t<G_Q4_0>(mp, scratch, counters, s);
+        case G_Q4_1: return matmul_t<G_Q4_1>(mp, scratch, counters, s);
+        case G_Q5_0: return matmul_t<G_Q5_0>(mp, scratch, counters, s);
+        case G_Q5_1: return matmul_t<G_Q5_1>(mp, scratch, counters, s);
+        case G_Q8_0: return matmul_t<G_Q8_0>(mp, scratch, counters, s);
+        case G_Q4K: return matmul_t<G_Q4K>(mp, scratch, counters, s);
+        case G_Q5K: return matmul_t<G_Q5K>(mp, scratch, counters, s);
+        case G_Q6K: return matmul_t<G_Q6K>(mp, scratch, counters, s);
         default: return hipErrorInvalidValue;
     }
 }
