@@ -353,43 +353,46 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_matmul(const MatmulParams p) 
 // ---------------------------------------------------------------------------------------
 // Batched product on the matrix cores (n >= MM_MIN input rows; the reference switches its
 // batches to a matrix-unit product the same way, gpu/mod.rs:33-41, metal.rs:153-197).
-// In the affine form, group g of weight row r is w = a q + b, q a small integer (exact in
-// f16); where b is a fixed multiple of a (Q4_0, Q5_0, Q8_0, Q6K) the offset is folded into
-// q, so sum_k w x = a sum q x (+ b sum x for Q4_1, Q5_1, Q4K, Q5K). The MFMAs compute
-// sum q x with x split into f16 parts, x = hi + lo 2^-12 (lo stored scaled by 2^12, so it
-// stays a normal f16; hi is zero where it would be subnormal): about 22 bits, each product
-// exact in f32, f32-level sums.
+// In the affine form, group g of weight row r is w = a q + b, q a small integer; so
+// sum_k w x = a sum q x + b sum x. The MFMAs compute sum q x with x split into f16 parts,
+// x = hi + lo 2^-12 (lo stored scaled by 2^12 so it keeps its 11 bits): about 22 bits,
+// each product exact in f32, f32-level sums.
 //
-// k_matmul_mm: a workgroup is four waves of 16 weight rows (64 rows), eight input rows and
-// a K range of at most MMK units of 256 columns. The range's x is staged once in LDS as 16
-// A rows: rows 0..7 the eight inputs' hi, rows 8..15 their lo, so one v_mfma_f32_16x16x32
-// _f16 over group g gives D[i][l] = sum hi_i q (i < 8) and sum lo_{i-8} q (i >= 8) for the
-// wave's 16 rows at once. Lane 16 c + l holds weights 8c .. 8c + 7 of group g of row r0 + l
-// as its B operand, unpacked from the ggml bytes in registers (bytes to f16 by v_perm_b32
-// onto 1024 + v, then one packed f16 subtraction that also removes the format's offset),
-// and D[4c + i][l]: c < 2 the hi sums of input 4c + i, c >= 2 the lo sums of input
-// 4(c - 2) + i. Per group each lane adds a_eff D[i] (a_eff = a, or a 2^-12 in lo lanes) and
-// b s[i] (s the group's sum of x, zero for lo lanes) to its four accumulators; the hi and
-// lo accumulators meet once at the end. The units' bytes are loaded MM_PF units ahead. Q6K
-// (a scale a 16 weights) takes two v_mfma_f32_16x16x16_f16 a group, one a half; F16 has
-// no scale and chains its MFMAs through the accumulators. K splits: their number depends
-// on rows and cols only; a split's partial is hi + lo of its units in order, and the row's
-// result the splits' partials added in split order, whether one workgroup runs the splits
-// one after another or ks workgroups run them at once and the last to finish (a device
-// counter per tile) adds them: an input row's bits depend on that row alone, never on n
-// or its place in the batch.
+// k_matmul_mm: a workgroup is W waves of 16 weight rows, eight input rows and a K range of
+// at most MMK units of 256 columns. The range's x is staged once in LDS as 16 A rows: rows
+// 0..7 the eight inputs' hi, rows 8..15 their lo, so one v_mfma_f32_16x16x32_f16 over group
+// g gives D[i][l] = sum hi_i q (i < 8) and sum lo_{i-8} q (i >= 8) for the wave's 16 rows at
+// once. Lane 16 c + l holds 8 weights of group g of row r0 + l (8c .. 8c + 7) as its B
+// operand, unpacked from the ggml bytes in registers, in the order 0, 2, 1, 3, 4, 6, 5, 7
+// (pairs of bytes 0, 2 and 1, 3 of a dword make the f16 pairs directly; staged x is
+// permuted alike, and the MFMA's sum over k is the group's either way): each field is put
+// under the f16 exponent of 1024 (one v_and_or_b32 for a pair of nibbles, v_perm_b32 for a
+// pair of bytes) and one packed f16 subtraction takes 1024 and the format's fixed offset
+// away (Q4_0 8, Q5_0 16, Q6K 32, Q8_0 -128 after a sign flip). D[4c + i][l] in lane
+// 16 c + l: c < 2 the hi sums of input 4c + i, c >= 2 the lo sums of input 4(c - 2) + i;
+// per group each lane adds a_eff D[i] (a_eff: a with the lo scale folded in) to four
+// accumulators. The b sum x terms (Q4_1, Q5_1: m; Q4K, Q5K: -dmin m_j) are a product over
+// groups of their own: a v_mfma_f32_16x16x4_f32 a half unit, A = the groups' sums of x
+// (rows 8..15 zero), B = the groups' b, accumulated across the range. Q6K (a scale a 16 weights) takes two
+// v_mfma_f32_16x16x16_f16 a group, one a half; F16 has no scale and chains its MFMAs
+// through the accumulators. The units' bytes are loaded MM_PF units ahead. K splits: their
+// number depends on rows and cols only; a split's partial is (hi + lo) + b terms of its
+// units, and the row's result the splits' partials added in split order, whether one
+// workgroup runs the splits one after another or ks workgroups run them at once and the
+// last to finish (a device counter per tile) adds them: an input row's bits depend on that
+// row alone, never on n or its place in the batch.
 constexpr float MM_LO = 4096.0f;   // lo = (x - hi) * MM_LO
 constexpr uint32_t MM_MIN = 8;     // batches of at least this many rows take the matrix cores
 constexpr uint32_t MMK = 8;        // units (256 columns) a K split at most
 constexpr uint32_t MM_XS = MMK * 256 + 8;  // LDS halves a staged x row: 16-byte reads of 16 rows on distinct banks
-constexpr uint32_t MM_PAR = MATMUL_COUNTERS;  // tiles (64 rows x 8 inputs) up to which K splits run in parallel
+constexpr uint32_t MM_PAR = MATMUL_COUNTERS;  // tiles (W x 16 rows x 8 inputs) up to which K splits run in parallel
 
 template <uint32_t TY>
 constexpr bool mm_type() {
     return TY == G_F16 || TY == G_Q8_0 || TY == G_Q4_0 || TY == G_Q4_1 || TY == G_Q5_0 || TY == G_Q5_1 ||
            TY == G_Q4K || TY == G_Q5K || TY == G_Q6K;
 }
-// Formats with a per-group b not a multiple of a: the product adds b sum x.
+// Formats whose b sum x terms take the f32 MFMA.
 template <uint32_t TY>
 constexpr bool mm_sum() {
     return TY == G_Q4_1 || TY == G_Q5_1 || TY == G_Q4K || TY == G_Q5K;
@@ -397,26 +400,50 @@ constexpr bool mm_sum() {
 // Dwords a lane holds of one unit (8 groups) of its row.
 template <uint32_t TY>
 constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 32 : TY == G_Q4_0 ? 32 : TY == G_Q4_1 ? 24
-                 : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 14 : 32;
-// Units loaded ahead.
+                 : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 14 : 29;
+// Units loaded ahead; waves a workgroup (eight where the registers allow four waves a SIMD).
 template <uint32_t TY>
 constexpr int MM_PF = MW<TY> <= 16 ? 3 : 2;
+template <uint32_t TY>
+constexpr int MM_W = MW<TY> <= 16 ? 8 : 4;
+// Bytes of a unit.
+template <uint32_t TY>
+constexpr uint32_t MM_UB = TY == G_F16 ? 512 : TY == G_Q8_0 ? 272 : TY == G_Q4_0 ? 144 : TY == G_Q4_1 ? 160
+                         : TY == G_Q5_0 ? 176 : TY == G_Q5_1 ? 192 : TY == G_Q4K ? 144 : TY == G_Q5K ? 176 : 210;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Bytes 0..3 of v, each 1024 + v_k - off exact in f16 (v_k < 256, off an f16 integer):
-// two f16 pairs.
+// The lane order of a dword's four bytes: 0, 2, 1, 3.
+// Bytes of v as f16 values 1024 + b - off, in that order (two f16 pairs).
 __device__ __forceinline__ u32x2 bytes_f16(uint32_t v, half2 off) {
-    const uint32_t e0 = __builtin_amdgcn_perm(0x64646464u, v, 0x05010400u);  // (b0 | 0x6400, b1 | 0x6400)
-    const uint32_t e1 = __builtin_amdgcn_perm(0x64646464u, v, 0x05030402u);  // (b2 | 0x6400, b3 | 0x6400)
+    const uint32_t e0 = __builtin_amdgcn_perm(0x64646464u, v, 0x04020400u);  // (0x6400 | b0, 0x6400 | b2)
+    const uint32_t e1 = __builtin_amdgcn_perm(0x64646464u, v, 0x04030401u);  // (0x6400 | b1, 0x6400 | b3)
     const half2 h0 = __builtin_bit_cast(half2, e0) - off, h1 = __builtin_bit_cast(half2, e1) - off;
     return u32x2{__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1)};
 }
-// Eight byte values (two dwords) as a B operand.
 __device__ __forceinline__ half8 bytes8_f16(uint32_t v0, uint32_t v1, half2 off) {
     const u32x2 a = bytes_f16(v0, off), b = bytes_f16(v1, off);
     return __builtin_bit_cast(half8, u32x4{a[0], a[1], b[0], b[1]});
+}
+// The field under m (within each 16 bits: 0x000f000f, 0x00f000f0) of bytes 0, 2 of v as f16
+// 1024 + f - off (exact): the field under the exponent of 1024 (one v_and_or_b32), then one
+// packed subtraction. (Fields as f16 subnormals, f 2^-24, would need no subtraction, but the
+// matrix cores multiply subnormals less exactly: about 1.7e-6 of a row's scale against 2e-7.)
+// (v & m) | e in one v_and_or_b32 (m in a VGPR, e an SGPR: the instruction may read one
+// SGPR and no literal, so the compiler otherwise splits it in two).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t e) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(m), "s"(e));
+    return r;
+}
+__device__ __forceinline__ uint32_t field_pair(uint32_t v, uint32_t m, half2 off, uint32_t extra = 0u) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, and_or(v, m, extra | 0x64006400u)) - off);
+}
+// Bytes 0, 2, then 1, 3 of two dwords.
+__device__ __forceinline__ half8 fields8(uint32_t v0, uint32_t v1, uint32_t m, half2 off) {
+    return __builtin_bit_cast(half8, u32x4{field_pair(v0, m, off), field_pair(v0 >> 8, m, off),
+                                           field_pair(v1, m, off), field_pair(v1 >> 8, m, off)});
 }
 // Four bits to bit 4 of bytes 0..3.
 __device__ __forceinline__ uint32_t bit4_spread(uint32_t b4) { return ((b4 * 0x00204081u) & 0x01010101u) << 4; }
@@ -434,6 +461,10 @@ __device__ __forceinline__ void align8(const uint8_t* p, const uint32_t* d, uint
     const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
     w0 = __builtin_amdgcn_alignbyte(d[1], d[0], sh);
     w1 = __builtin_amdgcn_alignbyte(d[2], d[1], sh);
+}
+// v[c] for the lane's c < 4.
+__device__ __forceinline__ uint32_t pick4(uint32_t c, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3) {
+    return c < 2 ? (c == 0 ? v0 : v1) : (c == 2 ? v2 : v3);
 }
 
 // Lane (c, row) loads of unit u (8 groups) of its row.
@@ -477,12 +508,13 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
         const uint8_t* bb = row + (size_t)u * BS;
         const u32x4 h = *(const u32x4*)bb;  // d, dmin, the 12 scale bytes
         d[0] = h[0]; d[1] = h[1]; d[2] = h[2]; d[3] = h[3];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const u32x2 v = *(const u32x2*)(bb + QS + 32 * k + 8 * c);
-            d[4 + 2 * k] = v[0];
-            d[5 + 2 * k] = v[1];
-        }
+        // qs in two 64-byte halves, 16 bytes a lane (a row's 64 bytes contiguous in one load):
+        // lane c takes piece (0, 2, 1, 3)[c] of each half, i.e. slices 2 (c / 2) and + 1 of
+        // chunk c % 2 (and of chunk 2 + c % 2); mm_fix swaps them into slice c of every chunk.
+        const uint32_t po = 32 * (c & 1) + 16 * (c >> 1);
+        const u32x4 va = *(const u32x4*)(bb + QS + po), vb = *(const u32x4*)(bb + QS + 64 + po);
+        d[4] = va[0]; d[5] = va[1]; d[6] = va[2]; d[7] = va[3];
+        d[8] = vb[0]; d[9] = vb[1]; d[10] = vb[2]; d[11] = vb[3];
         if constexpr (TY == G_Q5K) {
             const u32x2 v = *(const u32x2*)(bb + 16 + 8 * c);  // qh bytes 8c .. 8c + 7
             d[12] = v[0];
@@ -506,12 +538,62 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
     }
 }
 
-// Group j of a loaded unit for lane c: B operand(s), a (fl folded in) and b. Q6K gives two
-// half operands q4[0], q4[1] (16x16x16 MFMAs) and a0, a1.
+// After a unit's loads land: Q4K/Q5K lanes hold (chunk, slice) blocks (c % 2, 2 (c / 2)),
+// (c % 2, 2 (c / 2) + 1), (2 + c % 2, ...) in d[4..5], d[6..7], d[8..9], d[10..11]; lane
+// rows 2m and 2m + 1 (16 lanes each) swap d[6..7] and d[10..11] of the even row with
+// d[4..5] and d[8..9] of the odd row (v_permlane16_swap_b32: the odd row of its first
+// operand with the even row of its second), leaving chunk k's slice c in d[4 + 2k], d[5 + 2k].
 template <uint32_t TY>
-__device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const uint8_t* unit_base, int j, uint32_t c,
-                                         float fl, half8& q, half4 (&q4)[2], float& a0, float& a1, float& b) {
-    if constexpr (TY == G_F16) {
+__device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>]) {
+    if constexpr (TY == G_Q4K || TY == G_Q5K) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const auto a = __builtin_amdgcn_permlane16_swap(d[4 + t], d[6 + t], false, false);
+            d[4 + t] = a[0];
+            d[6 + t] = a[1];
+            const auto b = __builtin_amdgcn_permlane16_swap(d[8 + t], d[10 + t], false, false);
+            d[8 + t] = b[0];
+            d[10 + t] = b[1];
+        }
+    }
+}
+
+// What a unit's groups share: the scale factors and packed scale bytes (K-quants), and the
+// lane's two b values (groups c and 4 + c: B of the f32 MFMAs).
+struct MMUnit {
+    float dl = 0.0f, dh = 0.0f, b0 = 0.0f, b1 = 0.0f;
+    uint32_t scA = 0, scB = 0;
+};
+
+template <uint32_t TY>
+__device__ __forceinline__ MMUnit mm_unit(const uint32_t (&d)[MW<TY>], uint32_t c, float fl) {
+    MMUnit m;
+    if constexpr (TY == G_Q4K || TY == G_Q5K) {
+        // scale and min bytes of sub-blocks 0..3 and 4..7 (6 bits each, quant.rs:136-146)
+        const uint32_t s0 = d[1], s1 = d[2], s2 = d[3];
+        m.scA = s0 & 0x3f3f3f3fu;
+        m.scB = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+        const uint32_t mnA = s1 & 0x3f3f3f3fu, mnB = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+        const float dd = h2f(d[0] & 0xffffu) * fl, ndm = -h2f(d[0] >> 16);
+        m.dl = dd;
+        m.dh = TY == G_Q4K ? dd * 0.0625f : dd;  // Q4K high nibbles in place: 16 q
+        m.b0 = ndm * (float)((mnA >> (8 * c)) & 255u);
+        m.b1 = ndm * (float)((mnB >> (8 * c)) & 255u);
+    } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
+        constexpr int N = MW<TY> / 8;
+        m.b0 = h2f(pick4(c, d[2], d[N + 2], d[2 * N + 2], d[3 * N + 2]) >> 16);
+        m.b1 = h2f(pick4(c, d[4 * N + 2], d[5 * N + 2], d[6 * N + 2], d[7 * N + 2]) >> 16);
+    }
+    return m;
+}
+
+// Group j of a loaded unit for lane c: B operand(s) and a (fl and the field scale folded in).
+// Q6K gives two half operands q4[0], q4[1] (16x16x16 MFMAs) and a0, a1.
+template <uint32_t TY>
+__device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const MMUnit& m, const uint8_t* unit_base,
+                                         int j, uint32_t c, float fl, half8& q, half4 (&q4)[2], float& a0,
+                                         float& a1) {
+    if constexpr (TY == G_F16) {  // weights 8c .. 8c + 7 in order (x staged unpermuted)
         q = __builtin_bit_cast(half8, u32x4{d[4 * j], d[4 * j + 1], d[4 * j + 2], d[4 * j + 3]});
     } else if constexpr (TY == G_Q8_0) {
         const uint8_t* p = unit_base + 34 * j + 2 + 8 * c;
@@ -520,12 +602,12 @@ __device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const uint
         q = bytes8_f16(w0 ^ 0x80808080u, w1 ^ 0x80808080u, half2{(f16)1152.0f, (f16)1152.0f});
         a0 = h2f(d[4 * j + 3]) * fl;
     } else if constexpr (TY == G_Q4_0) {
+        // lanes 0, 1: low nibbles, lanes 2, 3: high nibbles (weights 16 ..), as q - 8
         const uint8_t* p = unit_base + 18 * j + 2 + 8 * (c & 1);
         uint32_t w0, w1;
         align8(p, &d[4 * j], w0, w1);
-        // lanes 0, 1: low nibbles, lanes 2, 3: high nibbles (weights 16 ..), as q - 8
         const uint32_t sh = c < 2 ? 0u : 4u;
-        q = bytes8_f16((w0 >> sh) & 0x0f0f0f0fu, (w1 >> sh) & 0x0f0f0f0fu, half2{(f16)1032.0f, (f16)1032.0f});
+        q = fields8(w0 >> sh, w1 >> sh, 0x000f000fu, half2{(f16)1032.0f, (f16)1032.0f});
         a0 = h2f(d[4 * j + 3]) * fl;
     } else if constexpr (TY == G_Q5_0) {
         const uint8_t* p = unit_base + 22 * j + 6 + 8 * (c & 1);
@@ -537,50 +619,34 @@ __device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const uint
         w1 = ((w1 >> sh) & 0x0f0f0f0fu) | bit4_spread(qh >> 4);
         q = bytes8_f16(w0, w1, half2{(f16)1040.0f, (f16)1040.0f});
         a0 = h2f(d[5 * j + 3]) * fl;
-    } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
-        constexpr uint32_t N = MW<TY> / 8;
-        uint32_t w0 = d[N * j], w1 = d[N * j + 1];
-        // lanes 0, 1: low nibbles, lanes 2, 3: high nibbles (weights 16 ..); Q5_1 adds qh byte c
-        // as bit 4. (The nibbles' scale must be the same across a group's k: the MFMA sums it.)
+    } else if constexpr (TY == G_Q4_1) {
         const uint32_t sh = c < 2 ? 0u : 4u;
-        w0 = (w0 >> sh) & 0x0f0f0f0fu;
-        w1 = (w1 >> sh) & 0x0f0f0f0fu;
-        if constexpr (TY == G_Q5_1) {
-            const uint32_t qh = (d[N * j + 3] >> (8 * c)) & 255u;
-            w0 |= bit4_spread(qh & 15u);
-            w1 |= bit4_spread(qh >> 4);
-        }
+        q = fields8(d[3 * j] >> sh, d[3 * j + 1] >> sh, 0x000f000fu, half2{(f16)1024.0f, (f16)1024.0f});
+        a0 = h2f(d[3 * j + 2] & 0xffffu) * fl;
+    } else if constexpr (TY == G_Q5_1) {
+        const uint32_t sh = c < 2 ? 0u : 4u;
+        const uint32_t qh = (d[4 * j + 3] >> (8 * c)) & 255u;  // qh byte c
+        const uint32_t w0 = ((d[4 * j] >> sh) & 0x0f0f0f0fu) | bit4_spread(qh & 15u);
+        const uint32_t w1 = ((d[4 * j + 1] >> sh) & 0x0f0f0f0fu) | bit4_spread(qh >> 4);
         q = bytes8_f16(w0, w1, half2{(f16)1024.0f, (f16)1024.0f});
-        a0 = h2f(d[N * j + 2] & 0xffffu) * fl;
-        b = h2f(d[N * j + 2] >> 16);
+        a0 = h2f(d[4 * j + 2] & 0xffffu) * fl;
     } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
         const int k = j / 2, hi = j % 2;
-        uint32_t w0 = d[4 + 2 * k], w1 = d[5 + 2 * k];
-        float sc16 = 1.0f;
+        const uint32_t v0 = d[4 + 2 * k], v1 = d[5 + 2 * k];
+        const half2 o = half2{(f16)1024.0f, (f16)1024.0f};
         if constexpr (TY == G_Q4K) {
-            const uint32_t m = hi ? 0xf0f0f0f0u : 0x0f0f0f0fu;  // high nibbles in place: 16 q
-            w0 &= m;
-            w1 &= m;
-            sc16 = hi ? 0.0625f : 1.0f;
-        } else {
-            w0 = ((w0 >> (4 * hi)) & 0x0f0f0f0fu) | (((d[12] >> j) & 0x01010101u) << 4);
-            w1 = ((w1 >> (4 * hi)) & 0x0f0f0f0fu) | (((d[13] >> j) & 0x01010101u) << 4);
+            q = fields8(v0, v1, hi ? 0x00f000f0u : 0x000f000fu, o);  // high nibbles in place: 16 q
+        } else {  // bit j of qh byte t is bit 4 of weight t
+            const uint32_t h0 = d[12] >> j, h1 = d[13] >> j;
+            const uint32_t n0 = hi ? v0 >> 4 : v0, n1 = hi ? v1 >> 4 : v1;
+            const uint32_t m4 = 0x000f000fu, b4 = 0x00010001u;
+            q = __builtin_bit_cast(half8, u32x4{field_pair(n0, m4, o, (h0 & b4) << 4),
+                                                field_pair(n0 >> 8, m4, o, ((h0 >> 8) & b4) << 4),
+                                                field_pair(n1, m4, o, (h1 & b4) << 4),
+                                                field_pair(n1 >> 8, m4, o, ((h1 >> 8) & b4) << 4)});
         }
-        q = bytes8_f16(w0, w1, half2{(f16)1024.0f, (f16)1024.0f});
-        // scale and min of sub-block j (6 bits each, quant.rs:136-146)
-        const uint32_t s0 = d[1], s1 = d[2], s2 = d[3];
-        uint32_t scb, mnb;
-        if (j < 4) {
-            scb = (s0 >> (8 * j)) & 63u;
-            mnb = (s1 >> (8 * j)) & 63u;
-        } else {
-            const int t = 8 * (j - 4);
-            scb = ((s2 >> t) & 15u) | (((s0 >> t) >> 2) & 0x30u);
-            mnb = ((s2 >> t) >> 4 & 15u) | (((s1 >> t) >> 2) & 0x30u);
-        }
-        const float dd = h2f(d[0] & 0xffffu), dm = h2f(d[0] >> 16);
-        a0 = dd * (float)scb * (fl * sc16);
-        b = -(dm * (float)mnb);
+        const uint32_t sc = ((j < 4 ? m.scA : m.scB) >> (8 * (j % 4))) & 255u;
+        a0 = (hi ? m.dh : m.dl) * (float)sc;
     } else {  // Q6K
         const int hh = j / 4, qr = j % 4, s = qr & 1;
         const uint32_t sh = (uint32_t)((uintptr_t)unit_base & 3u);
@@ -593,9 +659,8 @@ __device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const uint
         const uint32_t v0 = ((l0 >> ns) & 0x0f0f0f0fu) | (((h0 >> (2 * qr)) & 0x03030303u) << 4);
         const uint32_t v1 = ((l1 >> ns) & 0x0f0f0f0fu) | (((h1 >> (2 * qr)) & 0x03030303u) << 4);
         const half2 o = half2{(f16)1056.0f, (f16)1056.0f};
-        const u32x2 e0 = bytes_f16(v0, o), e1 = bytes_f16(v1, o);
-        q4[0] = __builtin_bit_cast(half4, e0);
-        q4[1] = __builtin_bit_cast(half4, e1);
+        q4[0] = __builtin_bit_cast(half4, bytes_f16(v0, o));
+        q4[1] = __builtin_bit_cast(half4, bytes_f16(v1, o));
         // scales (int8) 8 hh + 2 qr and + 1, d: bytes 192 .. 209 of the block
         const uint32_t sw = __builtin_amdgcn_alignbyte(d[25 + hh * 2 + (qr >> 1)], d[24 + hh * 2 + (qr >> 1)], sh);
         const uint32_t sp = sw >> (16 * (qr & 1));  // bytes 2 qr, 2 qr + 1 of the 4-byte window
@@ -616,18 +681,16 @@ struct MMParams {
 };
 
 template <uint32_t TY>
-__global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
-    constexpr bool SUM = mm_sum<TY>();
-    constexpr int PF = MM_PF<TY>;
-    constexpr uint32_t BS = TY == G_F16 ? 512 : TY == G_Q8_0 ? 272 : TY == G_Q4_0 ? 144 : TY == G_Q4_1 ? 160
-                          : TY == G_Q5_0 ? 176 : TY == G_Q5_1 ? 192 : TY == G_Q4K ? 144 : TY == G_Q5K ? 176 : 210;
+__global__ __launch_bounds__(64 * MM_W<TY>, 2) void k_matmul_mm(const MMParams p) {
+    constexpr bool SUM = mm_sum<TY>(), KP = TY != G_F16;
+    constexpr int PF = MM_PF<TY>, W = MM_W<TY>, NT = 64 * W;
     __shared__ __attribute__((aligned(16))) f16 xs[16 * MM_XS];
     __shared__ __attribute__((aligned(16))) float ss[SUM ? MMK * 8 * 16 : 4];
     __shared__ uint32_t last;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t c = lane >> 4, rl = lane & 15;
-    const uint32_t r = blockIdx.x * 64 + 16 * w + rl, i0 = blockIdx.y * 8;
-    const bool live = blockIdx.x * 64 + 16 * w < p.rows;  // the wave has rows
+    const uint32_t r = blockIdx.x * (16 * W) + 16 * w + rl, i0 = blockIdx.y * 8;
+    const bool live = blockIdx.x * (16 * W) + 16 * w < p.rows;  // the wave has rows
     const uint8_t* rowp = p.w + (size_t)min(r, p.rows - 1) * p.row_bytes;
     const float fl = c >= 2 ? 1.0f / MM_LO : 1.0f;
     const uint32_t kz0 = p.par ? blockIdx.z : 0, kz1 = p.par ? blockIdx.z + 1 : p.ks;
@@ -642,10 +705,10 @@ __global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
             for (int f = 0; f < PF; f++) mm_load<TY>(rowp, ua + min((uint32_t)f, nu - 1), c, pk[f]);
         }
         if (kz != kz0) __syncthreads();  // every wave is done with the previous split's x
-        // Stage x: thread pairs (input i, group g) of the range, 32 values each: hi, lo and
-        // (SUM) the group's sum in order.
+        // Stage x: thread pairs (input i, group g) of the range, 32 values each: hi, lo (in the
+        // lanes' k order) and (SUM) the group's sum in order.
         const uint32_t ng = 8 * nu;
-        for (uint32_t e = tid; e < 8 * ng; e += 256) {
+        for (uint32_t e = tid; e < 8 * ng; e += NT) {
             const uint32_t i = e / ng, g = e % ng, in = i0 + i;
             float v[32];
             if (in < p.n) {
@@ -671,9 +734,9 @@ __global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
                 half8 h, l;
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
-                    const float x = v[8 * k + t];
-                    f16 hv = (f16)x;
-                    if (__builtin_fabsf((float)hv) < 6.103515625e-05f) hv = (f16)0.0f;
+                    const int src = KP ? 8 * k + (t & 4) + ((t & 1) << 1) + ((t >> 1) & 1) : 8 * k + t;
+                    const float x = v[src];
+                    const f16 hv = (f16)x;
                     h[t] = hv;
                     l[t] = (f16)((x - (float)hv) * MM_LO);
                 }
@@ -682,21 +745,28 @@ __global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
             }
         }
         __syncthreads();
-        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, accb = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if (live) {
             for (uint32_t u0 = 0; u0 < nu; u0 += PF) {
 #pragma unroll
                 for (int f = 0; f < PF; f++) {
                     const uint32_t lu = u0 + f;
                     if (lu < nu) {
-                        const uint8_t* ub = rowp + (size_t)(ua + lu) * BS;
+                        const uint8_t* ub = rowp + (size_t)(ua + lu) * MM_UB<TY>;
+                        mm_fix<TY>(pk[f]);
+                        const MMUnit m = mm_unit<TY>(pk[f], c, fl);
+                        if constexpr (SUM) {  // sum_g b_g s_g over the unit's groups, 4 at a time
+                            const float s0 = ss[(lu * 8 + c) * 16 + rl], s1 = ss[(lu * 8 + 4 + c) * 16 + rl];
+                            accb = __builtin_amdgcn_mfma_f32_16x16x4f32(s0, m.b0, accb, 0, 0, 0);
+                            accb = __builtin_amdgcn_mfma_f32_16x16x4f32(s1, m.b1, accb, 0, 0, 0);
+                        }
 #pragma unroll
                         for (int j = 0; j < 8; j++) {
                             const uint32_t col = lu * 256 + 32 * j;
                             half8 q;
                             half4 q4[2];
-                            float a0 = 0.0f, a1 = 0.0f, b = 0.0f;
-                            mm_group<TY>(pk[f], ub, j, c, fl, q, q4, a0, a1, b);
+                            float a0 = 0.0f, a1 = 0.0f;
+                            mm_group<TY>(pk[f], m, ub, j, c, fl, q, q4, a0, a1);
                             if constexpr (TY == G_F16) {
                                 const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
                                 acc = mfma16(xa, q, acc);
@@ -711,15 +781,8 @@ __global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
                             } else {
                                 const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
                                 const f32x4 dv = mfma16(xa, q, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                                if constexpr (SUM) {
-                                    const f32x4 s = *(const f32x4*)&ss[(lu * 8 + j) * 16 + 4 * c];
 #pragma unroll
-                                    for (int i = 0; i < 4; i++)
-                                        acc[i] = __builtin_fmaf(b, s[i], __builtin_fmaf(a0, dv[i], acc[i]));
-                                } else {
-#pragma unroll
-                                    for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(a0, dv[i], acc[i]);
-                                }
+                                for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(a0, dv[i], acc[i]);
                             }
                         }
                     }
@@ -734,10 +797,12 @@ __global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[i] *= fl;
         }
-        // the split's partial: hi + lo, in lanes c < 2 (input 4c + i); then splits in order
+        // the split's partial in lanes c < 2 (input 4c + i): hi + lo, then the b terms; then
+        // the splits in order
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float pt = acc[i] + __shfl_xor(acc[i], 32, 64);
+            float pt = acc[i] + __shfl_xor(acc[i], 32, 64);
+            if constexpr (SUM) pt += accb[i];
             tot[i] = kz == kz0 ? pt : tot[i] + pt;
         }
     }
@@ -766,32 +831,60 @@ __global__ __launch_bounds__(256, 2) void k_matmul_mm(const MMParams p) {
     }
     __syncthreads();
     if (!last) return;
-    for (uint32_t e = tid; e < 512; e += 256) {
-        const uint32_t rr = blockIdx.x * 64 + e % 64, in = i0 + e / 64;
-        if (rr < p.rows && in < p.n) {
-            const float* src = p.part + (size_t)in * p.rows + rr;
-            const size_t stride = (size_t)p.npad * p.rows;
-            float s = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (uint32_t k = 1; k < p.ks; k++)
-                s += __hip_atomic_load(src + k * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            p.out[(size_t)in * p.rows + rr] = s;
-        }
+    // The tile's 8 x 16 W outputs, two a thread; eight splits' loads in flight at a time.
+    const size_t stride = (size_t)p.npad * p.rows;
+    float sum[2] = {0.0f, 0.0f};
+    bool ok[2];
+    const float* src[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t e = tid + h * NT, rr = blockIdx.x * (16 * W) + e % (16 * W), in = i0 + e / (16 * W);
+        ok[h] = rr < p.rows && in < p.n;
+        src[h] = p.part + (size_t)min(in, p.npad - 1) * p.rows + min(rr, p.rows - 1);
+    }
+    for (uint32_t k0 = 0; k0 < p.ks; k0 += 8) {
+        float v[2][8];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                v[h][t] = k0 + t < p.ks ? __hip_atomic_load(src[h] + (k0 + t) * stride, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT)
+                                        : 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                if (k0 + t < p.ks) sum[h] = k0 + t == 0 ? v[h][t] : sum[h] + v[h][t];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t e = tid + h * NT, rr = blockIdx.x * (16 * W) + e % (16 * W), in = i0 + e / (16 * W);
+        if (ok[h]) p.out[(size_t)in * p.rows + rr] = sum[h];
     }
     if (tid == 0) __hip_atomic_store(&p.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Rows a workgroup of the format takes.
+static uint32_t mm_rows(uint32_t type) {
+    switch (type) {
+        case G_Q4K: return 16 * MM_W<G_Q4K>;
+        case G_Q5K: return 16 * MM_W<G_Q5K>;
+        default: return 64;  // MW > 16: four waves
+    }
+}
 // K splits of a product: about two workgroups a CU from the rows alone (never from n), each
 // split at most MMK units.
-static uint32_t mm_ks(uint32_t rows, uint32_t cols) {
-    const uint32_t rt = (rows + 63) / 64, units = cols / 256;
-    uint32_t ks = (512u + rt / 2) / rt;
+static uint32_t mm_ks(uint32_t type, uint32_t rows, uint32_t cols) {
+    const uint32_t rt = (rows + mm_rows(type) - 1) / mm_rows(type), units = cols / 256;
+    uint32_t ks = max(512u / rt, 1u);
     ks = max(ks, (units + MMK - 1) / MMK);
     ks = min(ks, units);
     return max(ks, 1u);
 }
-static bool mm_par(uint32_t rows, uint32_t cols, uint32_t n) {
-    const uint32_t rt = (rows + 63) / 64, nt = (n + 7) / 8;
-    return mm_ks(rows, cols) > 1 && (uint64_t)rt * nt <= MM_PAR;
+static bool mm_par(uint32_t type, uint32_t rows, uint32_t cols, uint32_t n) {
+    const uint32_t rt = (rows + mm_rows(type) - 1) / mm_rows(type), nt = (n + 7) / 8;
+    return mm_ks(type, rows, cols) > 1 && (uint64_t)rt * nt <= MM_PAR;
 }
 
 bool matmul_uses_mm(uint32_t type, uint32_t cols, uint32_t n) {
@@ -803,18 +896,19 @@ bool matmul_uses_mm(uint32_t type, uint32_t cols, uint32_t n) {
 }
 
 size_t matmul_scratch_bytes(uint32_t type, uint32_t rows, uint32_t cols, uint32_t n) {
-    if (!matmul_uses_mm(type, cols, n) || !mm_par(rows, cols, n)) return 0;
-    return (size_t)mm_ks(rows, cols) * ((n + 7) / 8 * 8) * rows * sizeof(float);
+    if (!matmul_uses_mm(type, cols, n) || !mm_par(type, rows, cols, n)) return 0;
+    return (size_t)mm_ks(type, rows, cols) * ((n + 7) / 8 * 8) * rows * sizeof(float);
 }
 
 template <uint32_t TY>
 static hipError_t matmul_mm_go(const MatmulParams& mp, void* scratch, uint32_t* counters, hipStream_t s) {
-    const uint32_t ks = mm_ks(mp.rows, mp.cols), rt = (mp.rows + 63) / 64, nt = (mp.n + 7) / 8;
-    const bool par = mm_par(mp.rows, mp.cols, mp.n);
+    const uint32_t ks = mm_ks(TY, mp.rows, mp.cols), rt = (mp.rows + 16 * MM_W<TY> - 1) / (16 * MM_W<TY>);
+    const uint32_t nt = (mp.n + 7) / 8;
+    const bool par = mm_par(TY, mp.rows, mp.cols, mp.n);
     if (par && (!scratch || !counters)) return hipErrorInvalidValue;
     const MMParams q{mp.w, mp.x, mp.out, (float*)scratch, counters, mp.rows, mp.cols, mp.n, nt * 8, mp.row_bytes,
                      mp.cols / 256, ks, par ? 1u : 0u};
-    hipLaunchKernelGGL((k_matmul_mm<TY>), dim3(rt, nt, par ? ks : 1), dim3(256), 0, s, q);
+    hipLaunchKernelGGL((k_matmul_mm<TY>), dim3(rt, nt, par ? ks : 1), dim3(64 * MM_W<TY>), 0, s, q);
     return hipGetLastError();
 }
 
