@@ -403,7 +403,7 @@ constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 32 : TY == G_Q4_0 ? 32 : TY
                  : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 14 : 29;
 // Units loaded ahead; waves a workgroup (eight where the registers allow four waves a SIMD).
 template <uint32_t TY>
-constexpr int MM_PF = MW<TY> <= 16 ? 3 : 2;
+constexpr int MM_PF = 2;
 template <uint32_t TY>
 constexpr int MM_W = MW<TY> <= 16 ? 8 : 4;
 // Bytes of a unit.
@@ -439,6 +439,12 @@ __device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t e) {
 }
 __device__ __forceinline__ uint32_t field_pair(uint32_t v, uint32_t m, half2 off, uint32_t extra = 0u) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, and_or(v, m, extra | 0x64006400u)) - off);
+}
+// As field_pair, times a scale in one packed FMA: (1024 + f) c1 + c2 with c2 = -1024 c1, exact
+// while f c1 is an f16 integer (K-quant sub-block scale times field: at most 63 x 31).
+__device__ __forceinline__ uint32_t field_pair_sc(uint32_t v, uint32_t m, half2 c1, half2 c2, uint32_t extra = 0u) {
+    const half2 e = __builtin_bit_cast(half2, and_or(v, m, extra | 0x64006400u));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(e, c1, c2));
 }
 // Bytes 0, 2, then 1, 3 of two dwords.
 __device__ __forceinline__ half8 fields8(uint32_t v0, uint32_t v1, uint32_t m, half2 off) {
@@ -561,7 +567,7 @@ __device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>]) {
 // What a unit's groups share: the scale factors and packed scale bytes (K-quants), and the
 // lane's two b values (groups c and 4 + c: B of the f32 MFMAs).
 struct MMUnit {
-    float dl = 0.0f, dh = 0.0f, b0 = 0.0f, b1 = 0.0f;
+    float dl = 0.0f, b0 = 0.0f, b1 = 0.0f;
     uint32_t scA = 0, scB = 0;
 };
 
@@ -576,7 +582,6 @@ __device__ __forceinline__ MMUnit mm_unit(const uint32_t (&d)[MW<TY>], uint32_t 
         const uint32_t mnA = s1 & 0x3f3f3f3fu, mnB = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
         const float dd = h2f(d[0] & 0xffffu) * fl, ndm = -h2f(d[0] >> 16);
         m.dl = dd;
-        m.dh = TY == G_Q4K ? dd * 0.0625f : dd;  // Q4K high nibbles in place: 16 q
         m.b0 = ndm * (float)((mnA >> (8 * c)) & 255u);
         m.b1 = ndm * (float)((mnB >> (8 * c)) & 255u);
     } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
@@ -633,20 +638,29 @@ __device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const MMUn
     } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
         const int k = j / 2, hi = j % 2;
         const uint32_t v0 = d[4 + 2 * k], v1 = d[5 + 2 * k];
-        const half2 o = half2{(f16)1024.0f, (f16)1024.0f};
+        // B = q sc_j (an f16 integer): the sub-block scale rides in the unpacking FMA, so the
+        // unit's eight MFMAs chain through one accumulator and d scales the unit once.
+        // (sc_j, sc_j) from its byte under the exponent of 1024: (1024 + sc) s - 1024 s, with
+        // s = 1/16 for Q4K's high nibbles, which stay in place (16 q).
+        const uint32_t b = (uint32_t)(j % 4);
+        const half2 e = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, j < 4 ? m.scA : m.scB,
+                                                                        0x04000400u | b | (b << 16)));
+        const f16 s16 = (TY == G_Q4K && hi) ? (f16)0.0625f : (f16)1.0f;
+        const half2 c1 = __builtin_elementwise_fma(e, half2{s16, s16}, half2{(f16)-1024.0f * s16, (f16)-1024.0f * s16});
+        const half2 c2 = c1 * half2{(f16)-1024.0f, (f16)-1024.0f};
         if constexpr (TY == G_Q4K) {
-            q = fields8(v0, v1, hi ? 0x00f000f0u : 0x000f000fu, o);  // high nibbles in place: 16 q
+            const uint32_t mk = hi ? 0x00f000f0u : 0x000f000fu;
+            q = __builtin_bit_cast(half8, u32x4{field_pair_sc(v0, mk, c1, c2), field_pair_sc(v0 >> 8, mk, c1, c2),
+                                                field_pair_sc(v1, mk, c1, c2), field_pair_sc(v1 >> 8, mk, c1, c2)});
         } else {  // bit j of qh byte t is bit 4 of weight t
             const uint32_t h0 = d[12] >> j, h1 = d[13] >> j;
             const uint32_t n0 = hi ? v0 >> 4 : v0, n1 = hi ? v1 >> 4 : v1;
             const uint32_t m4 = 0x000f000fu, b4 = 0x00010001u;
-            q = __builtin_bit_cast(half8, u32x4{field_pair(n0, m4, o, (h0 & b4) << 4),
-                                                field_pair(n0 >> 8, m4, o, ((h0 >> 8) & b4) << 4),
-                                                field_pair(n1, m4, o, (h1 & b4) << 4),
-                                                field_pair(n1 >> 8, m4, o, ((h1 >> 8) & b4) << 4)});
+            q = __builtin_bit_cast(half8, u32x4{field_pair_sc(n0, m4, c1, c2, (h0 & b4) << 4),
+                                                field_pair_sc(n0 >> 8, m4, c1, c2, ((h0 >> 8) & b4) << 4),
+                                                field_pair_sc(n1, m4, c1, c2, (h1 & b4) << 4),
+                                                field_pair_sc(n1 >> 8, m4, c1, c2, ((h1 >> 8) & b4) << 4)});
         }
-        const uint32_t sc = ((j < 4 ? m.scA : m.scB) >> (8 * (j % 4))) & 255u;
-        a0 = (hi ? m.dh : m.dl) * (float)sc;
     } else {  // Q6K
         const int hh = j / 4, qr = j % 4, s = qr & 1;
         const uint32_t sh = (uint32_t)((uintptr_t)unit_base & 3u);
@@ -760,6 +774,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, 2) void k_matmul_mm(const MMParams p
                             accb = __builtin_amdgcn_mfma_f32_16x16x4f32(s0, m.b0, accb, 0, 0, 0);
                             accb = __builtin_amdgcn_mfma_f32_16x16x4f32(s1, m.b1, accb, 0, 0, 0);
                         }
+                        f32x4 accu = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                         for (int j = 0; j < 8; j++) {
                             const uint32_t col = lu * 256 + 32 * j;
@@ -767,7 +782,10 @@ __global__ __launch_bounds__(64 * MM_W<TY>, 2) void k_matmul_mm(const MMParams p
                             half4 q4[2];
                             float a0 = 0.0f, a1 = 0.0f;
                             mm_group<TY>(pk[f], m, ub, j, c, fl, q, q4, a0, a1);
-                            if constexpr (TY == G_F16) {
+                            if constexpr (TY == G_Q4K || TY == G_Q5K) {
+                                const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
+                                accu = mfma16(xa, q, accu);
+                            } else if constexpr (TY == G_F16) {
                                 const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
                                 acc = mfma16(xa, q, acc);
                             } else if constexpr (TY == G_Q6K) {
@@ -784,6 +802,10 @@ __global__ __launch_bounds__(64 * MM_W<TY>, 2) void k_matmul_mm(const MMParams p
 #pragma unroll
                                 for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(a0, dv[i], acc[i]);
                             }
+                        }
+                        if constexpr (TY == G_Q4K || TY == G_Q5K) {
+#pragma unroll
+                            for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(m.dl, accu[i], acc[i]);
                         }
                     }
                     // the unit's registers are free: load into them directly (a load hoisted
