@@ -695,7 +695,7 @@ struct MMParams {
 };
 
 template <uint32_t TY>
-__global__ __launch_bounds__(64 * MM_W<TY>, 2) void k_matmul_mm(const MMParams p) {
+__global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const MMParams p) {  // two workgroups a CU
     constexpr bool SUM = mm_sum<TY>(), KP = TY != G_F16;
     constexpr int PF = MM_PF<TY>, W = MM_W<TY>, NT = 64 * W;
     __shared__ __attribute__((aligned(16))) f16 xs[16 * MM_XS];
@@ -719,43 +719,45 @@ __global__ __launch_bounds__(64 * MM_W<TY>, 2) void k_matmul_mm(const MMParams p
             for (int f = 0; f < PF; f++) mm_load<TY>(rowp, ua + min((uint32_t)f, nu - 1), c, pk[f]);
         }
         if (kz != kz0) __syncthreads();  // every wave is done with the previous split's x
-        // Stage x: thread pairs (input i, group g) of the range, 32 values each: hi, lo (in the
-        // lanes' k order) and (SUM) the group's sum in order.
-        const uint32_t ng = 8 * nu;
-        for (uint32_t e = tid; e < 8 * ng; e += NT) {
-            const uint32_t i = e / ng, g = e % ng, in = i0 + i;
-            float v[32];
-            if (in < p.n) {
-                const float4* src = (const float4*)(p.x + (size_t)in * p.cols + (size_t)ua * 256 + 32 * g);
+        // Stage x: float4 q of the range (input q / (64 nu), columns 4 (q % (64 nu)) ..), read
+        // coalesced (consecutive lanes, consecutive 16 bytes), as hi and lo in the lanes' k order
+        // (within each 8 columns: 0, 2, 1, 3, 4, 6, 5, 7, so a float4's four values stay
+        // together); (SUM) a group's sum over the 8 lanes that hold it, in a fixed tree.
+        const uint32_t q4 = 64 * nu;  // float4s an input row of the range
+        constexpr int XB = W == 8 ? 4 : 8;  // loads in flight a thread (eight waves: a split's all)
+        for (uint32_t q0 = tid; q0 < 8 * q4; q0 += XB * NT) {
+            float4 v[XB];
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const float4 t = src[k];
-                    v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
-                }
-            } else {
-#pragma unroll
-                for (int k = 0; k < 32; k++) v[k] = 0.0f;
-            }
-            if constexpr (SUM) {
-                float s = v[0];
-#pragma unroll
-                for (int k = 1; k < 32; k++) s += v[k];
-                ss[g * 16 + i] = s;
-                ss[g * 16 + 8 + i] = 0.0f;
+            for (int t = 0; t < XB; t++) {
+                const uint32_t q = q0 + t * NT, in = i0 + q / q4;
+                v[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (q < 8 * q4 && in < p.n)
+                    v[t] = *(const float4*)(p.x + (size_t)in * p.cols + (size_t)ua * 256 + 4 * (q % q4));
             }
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                half8 h, l;
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const int src = KP ? 8 * k + (t & 4) + ((t & 1) << 1) + ((t >> 1) & 1) : 8 * k + t;
-                    const float x = v[src];
-                    const f16 hv = (f16)x;
-                    h[t] = hv;
-                    l[t] = (f16)((x - (float)hv) * MM_LO);
+            for (int t = 0; t < XB; t++) {
+                const uint32_t q = q0 + t * NT, i = q / q4, cq = q % q4;
+                if (q >= 8 * q4) break;  // uniform: 8 q4 is a multiple of NT
+                if constexpr (SUM) {
+                    float sg = ((v[t].x + v[t].y) + v[t].z) + v[t].w;
+                    sg += __shfl_xor(sg, 1, 64);
+                    sg += __shfl_xor(sg, 2, 64);
+                    sg += __shfl_xor(sg, 4, 64);
+                    if ((cq & 7) == 0) {
+                        ss[(cq / 8) * 16 + i] = sg;
+                        ss[(cq / 8) * 16 + 8 + i] = 0.0f;
+                    }
                 }
-                *(half8*)&xs[i * MM_XS + 32 * g + 8 * k] = h;
-                *(half8*)&xs[(8 + i) * MM_XS + 32 * g + 8 * k] = l;
+                const float xs4[4] = {v[t].x, KP ? v[t].z : v[t].y, KP ? v[t].y : v[t].z, v[t].w};
+                half4 h, l;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const f16 hv = (f16)xs4[e];
+                    h[e] = hv;
+                    l[e] = (f16)((xs4[e] - (float)hv) * MM_LO);
+                }
+                *(half4*)&xs[i * MM_XS + 4 * cq] = h;
+                *(half4*)&xs[(8 + i) * MM_XS + 4 * cq] = l;
             }
         }
         __syncthreads();
