@@ -359,7 +359,7 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_matmul(const MatmulParams p) 
 // each product exact in f32, f32-level sums.
 //
 // k_matmul_mm: a workgroup is W waves of 16 weight rows, eight input rows and a K range of
-// at most MMK units of 256 columns. The range's x is staged once in LDS as 16 A rows: rows
+// at most MM_K units of 256 columns. The range's x is staged once in LDS as 16 A rows: rows
 // 0..7 the eight inputs' hi, rows 8..15 their lo, so one v_mfma_f32_16x16x32_f16 over group
 // g gives D[i][l] = sum hi_i q (i < 8) and sum lo_{i-8} q (i >= 8) for the wave's 16 rows at
 // once. Lane 16 c + l holds 8 weights of group g of row r0 + l (8c .. 8c + 7) as its B
@@ -383,8 +383,13 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_matmul(const MatmulParams p) 
 // row alone, never on n or its place in the batch.
 constexpr float MM_LO = 4096.0f;   // lo = (x - hi) * MM_LO
 constexpr uint32_t MM_MIN = 8;     // batches of at least this many rows take the matrix cores
-constexpr uint32_t MMK = 8;        // units (256 columns) a K split at most
-constexpr uint32_t MM_XS = MMK * 256 + 8;  // LDS halves a staged x row: 16-byte reads of 16 rows on distinct banks
+// Units (256 columns) a K split at most: the staged x takes 16 rows x (256 MM_K + 8) halves of
+// LDS (the 8: 16-byte reads of 16 rows on distinct banks); the K-quants also pass each unit's
+// bytes through LDS, so their splits are shorter.
+template <uint32_t TY>
+constexpr uint32_t MM_K = TY == G_Q4K || TY == G_Q5K ? 4 : 8;
+template <uint32_t TY>
+constexpr uint32_t MM_XS = MM_K<TY> * 256 + 8;
 constexpr uint32_t MM_PAR = MATMUL_COUNTERS;  // tiles (W x 16 rows x 8 inputs) up to which K splits run in parallel
 
 template <uint32_t TY>
@@ -510,21 +515,17 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
             if constexpr (TY == G_Q5_1) d[N * j + 3] = ld32(bb + 4);  // qh
         }
     } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
-        constexpr uint32_t BS = TY == G_Q4K ? 144 : 176, QS = TY == G_Q4K ? 16 : 48;
-        const uint8_t* bb = row + (size_t)u * BS;
-        const u32x4 h = *(const u32x4*)bb;  // d, dmin, the 12 scale bytes
-        d[0] = h[0]; d[1] = h[1]; d[2] = h[2]; d[3] = h[3];
-        // qs in two 64-byte halves, 16 bytes a lane (a row's 64 bytes contiguous in one load):
-        // lane c takes piece (0, 2, 1, 3)[c] of each half, i.e. slices 2 (c / 2) and + 1 of
-        // chunk c % 2 (and of chunk 2 + c % 2); mm_fix swaps them into slice c of every chunk.
-        const uint32_t po = 32 * (c & 1) + 16 * (c >> 1);
-        const u32x4 va = *(const u32x4*)(bb + QS + po), vb = *(const u32x4*)(bb + QS + 64 + po);
-        d[4] = va[0]; d[5] = va[1]; d[6] = va[2]; d[7] = va[3];
-        d[8] = vb[0]; d[9] = vb[1]; d[10] = vb[2]; d[11] = vb[3];
-        if constexpr (TY == G_Q5K) {
-            const u32x2 v = *(const u32x2*)(bb + 16 + 8 * c);  // qh bytes 8c .. 8c + 7
-            d[12] = v[0];
-            d[13] = v[1];
+        // Row-contiguous lane order (the memory path coalesces consecutive lanes: 64 bytes of
+        // one row a lane quad), 16-byte pieces 4 l + (lane & 3) of the unit for l < 3 (the last
+        // load's pieces past the unit repeat its last); `row` is the lane quad's row, and
+        // mm_fix moves the pieces through LDS into the matrix-core layout.
+        constexpr uint32_t NP = MM_UB<TY> / 16;  // pieces a unit: 9 (Q4K), 11 (Q5K)
+        const uint8_t* bb = row + (size_t)u * MM_UB<TY>;
+        const uint32_t pq = threadIdx.x & 3u;
+#pragma unroll
+        for (int l = 0; l < 3; l++) {
+            const u32x4 v = *(const u32x4*)(bb + 16 * min(4 * l + pq, NP - 1));
+            d[4 * l] = v[0]; d[4 * l + 1] = v[1]; d[4 * l + 2] = v[2]; d[4 * l + 3] = v[3];
         }
     } else {  // Q6K: lane c's weights 4c .. 4c + 3 and 16 + 4c .. of each 32-weight run
         const uint8_t* bb = row + (size_t)u * 210;
@@ -544,22 +545,33 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
     }
 }
 
-// After a unit's loads land: Q4K/Q5K lanes hold (chunk, slice) blocks (c % 2, 2 (c / 2)),
-// (c % 2, 2 (c / 2) + 1), (2 + c % 2, ...) in d[4..5], d[6..7], d[8..9], d[10..11]; lane
-// rows 2m and 2m + 1 (16 lanes each) swap d[6..7] and d[10..11] of the even row with
-// d[4..5] and d[8..9] of the odd row (v_permlane16_swap_b32: the odd row of its first
-// operand with the even row of its second), leaving chunk k's slice c in d[4 + 2k], d[5 + 2k].
+// After a unit's loads land (K-quants): each lane quad's three pieces go to the wave's LDS
+// rows (row q = lane / 4, the unit's bytes in order; row stride 144 or 176 bytes puts the 16
+// rows' reads of one offset on distinct banks), and each lane reads back what the matrix-core
+// layout gives it: the header (d, dmin, scales) and slice c of each 32-byte qs chunk (Q5K also
+// qh bytes 8c .. 8c + 7), into d[0..3], d[4 + 2k..5 + 2k] (chunk k) and d[12..13].
 template <uint32_t TY>
-__device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>]) {
+__device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>], uint8_t* wt, uint32_t c, uint32_t rl) {
     if constexpr (TY == G_Q4K || TY == G_Q5K) {
+        constexpr uint32_t UB = MM_UB<TY>, NP = UB / 16, QS = TY == G_Q4K ? 16 : 48;
+        const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u;
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const auto a = __builtin_amdgcn_permlane16_swap(d[4 + t], d[6 + t], false, false);
-            d[4 + t] = a[0];
-            d[6 + t] = a[1];
-            const auto b = __builtin_amdgcn_permlane16_swap(d[8 + t], d[10 + t], false, false);
-            d[8 + t] = b[0];
-            d[10 + t] = b[1];
+        for (int l = 0; l < 3; l++)
+            *(u32x4*)(wt + q * UB + 16 * min(4 * l + pq, NP - 1)) =
+                u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
+        const uint8_t* rw = wt + rl * UB;
+        const u32x4 h = *(const u32x4*)rw;
+        d[0] = h[0]; d[1] = h[1]; d[2] = h[2]; d[3] = h[3];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const u32x2 v = *(const u32x2*)(rw + QS + 32 * k + 8 * c);
+            d[4 + 2 * k] = v[0];
+            d[5 + 2 * k] = v[1];
+        }
+        if constexpr (TY == G_Q5K) {
+            const u32x2 v = *(const u32x2*)(rw + 16 + 8 * c);
+            d[12] = v[0];
+            d[13] = v[1];
         }
     }
 }
@@ -698,14 +710,19 @@ template <uint32_t TY>
 __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const MMParams p) {  // two workgroups a CU
     constexpr bool SUM = mm_sum<TY>(), KP = TY != G_F16;
     constexpr int PF = MM_PF<TY>, W = MM_W<TY>, NT = 64 * W;
-    __shared__ __attribute__((aligned(16))) f16 xs[16 * MM_XS];
-    __shared__ __attribute__((aligned(16))) float ss[SUM ? MMK * 8 * 16 : 4];
+    constexpr uint32_t XS = MM_XS<TY>;
+    __shared__ __attribute__((aligned(16))) f16 xs[16 * XS];
+    __shared__ __attribute__((aligned(16))) float ss[SUM ? MM_K<TY> * 8 * 16 : 4];
+    constexpr bool KQ = TY == G_Q4K || TY == G_Q5K;  // units pass through LDS (mm_fix)
+    __shared__ __attribute__((aligned(16))) uint8_t wtb[KQ ? W * 16 * MM_UB<TY> : 16];
     __shared__ uint32_t last;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t c = lane >> 4, rl = lane & 15;
-    const uint32_t r = blockIdx.x * (16 * W) + 16 * w + rl, i0 = blockIdx.y * 8;
-    const bool live = blockIdx.x * (16 * W) + 16 * w < p.rows;  // the wave has rows
-    const uint8_t* rowp = p.w + (size_t)min(r, p.rows - 1) * p.row_bytes;
+    const uint32_t r0 = blockIdx.x * (16 * W) + 16 * w, r = r0 + rl, i0 = blockIdx.y * 8;
+    const bool live = r0 < p.rows;  // the wave has rows
+    // the rows a lane loads: its matrix-core row, or (KQ) its lane quad's
+    const uint8_t* rowp = p.w + (size_t)min(KQ ? r0 + (lane >> 2) : r, p.rows - 1) * p.row_bytes;
+    uint8_t* wt = wtb + (KQ ? w * 16 * MM_UB<TY> : 0);
     const float fl = c >= 2 ? 1.0f / MM_LO : 1.0f;
     const uint32_t kz0 = p.par ? blockIdx.z : 0, kz1 = p.par ? blockIdx.z + 1 : p.ks;
     float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -756,8 +773,8 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                     h[e] = hv;
                     l[e] = (f16)((xs4[e] - (float)hv) * MM_LO);
                 }
-                *(half4*)&xs[i * MM_XS + 4 * cq] = h;
-                *(half4*)&xs[(8 + i) * MM_XS + 4 * cq] = l;
+                *(half4*)&xs[i * XS + 4 * cq] = h;
+                *(half4*)&xs[(8 + i) * XS + 4 * cq] = l;
             }
         }
         __syncthreads();
@@ -769,7 +786,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                     const uint32_t lu = u0 + f;
                     if (lu < nu) {
                         const uint8_t* ub = rowp + (size_t)(ua + lu) * MM_UB<TY>;
-                        mm_fix<TY>(pk[f]);
+                        mm_fix<TY>(pk[f], wt, c, rl);
                         const MMUnit m = mm_unit<TY>(pk[f], c, fl);
                         if constexpr (SUM) {  // sum_g b_g s_g over the unit's groups, 4 at a time
                             const float s0 = ss[(lu * 8 + c) * 16 + rl], s1 = ss[(lu * 8 + 4 + c) * 16 + rl];
@@ -785,21 +802,21 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                             float a0 = 0.0f, a1 = 0.0f;
                             mm_group<TY>(pk[f], m, ub, j, c, fl, q, q4, a0, a1);
                             if constexpr (TY == G_Q4K || TY == G_Q5K) {
-                                const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
+                                const half8 xa = *(const half8*)&xs[rl * XS + col + 8 * c];
                                 accu = mfma16(xa, q, accu);
                             } else if constexpr (TY == G_F16) {
-                                const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
+                                const half8 xa = *(const half8*)&xs[rl * XS + col + 8 * c];
                                 acc = mfma16(xa, q, acc);
                             } else if constexpr (TY == G_Q6K) {
-                                const half4 x0 = *(const half4*)&xs[rl * MM_XS + col + 4 * c];
-                                const half4 x1 = *(const half4*)&xs[rl * MM_XS + col + 16 + 4 * c];
+                                const half4 x0 = *(const half4*)&xs[rl * XS + col + 4 * c];
+                                const half4 x1 = *(const half4*)&xs[rl * XS + col + 16 + 4 * c];
                                 const f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                                 const f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x16f16(x0, q4[0], z, 0, 0, 0);
                                 const f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x16f16(x1, q4[1], z, 0, 0, 0);
 #pragma unroll
                                 for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(a1, d1[i], __builtin_fmaf(a0, d0[i], acc[i]));
                             } else {
-                                const half8 xa = *(const half8*)&xs[rl * MM_XS + col + 8 * c];
+                                const half8 xa = *(const half8*)&xs[rl * XS + col + 8 * c];
                                 const f32x4 dv = mfma16(xa, q, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                                 for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(a0, dv[i], acc[i]);
@@ -898,11 +915,12 @@ static uint32_t mm_rows(uint32_t type) {
     }
 }
 // K splits of a product: about two workgroups a CU from the rows alone (never from n), each
-// split at most MMK units.
+// split at most MM_K units.
 static uint32_t mm_ks(uint32_t type, uint32_t rows, uint32_t cols) {
     const uint32_t rt = (rows + mm_rows(type) - 1) / mm_rows(type), units = cols / 256;
+    const uint32_t kmax = type == G_Q4K || type == G_Q5K ? MM_K<G_Q4K> : MM_K<G_Q8_0>;
     uint32_t ks = max(512u / rt, 1u);
-    ks = max(ks, (units + MMK - 1) / MMK);
+    ks = max(ks, (units + kmax - 1) / kmax);
     ks = min(ks, units);
     return max(ks, 1u);
 }
