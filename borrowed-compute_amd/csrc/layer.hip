@@ -546,30 +546,33 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
 }
 
 // After a unit's loads land (K-quants): each lane quad's three pieces go to the wave's LDS
-// rows (row q = lane / 4, the unit's bytes in order; row stride 144 or 176 bytes puts the 16
-// rows' reads of one offset on distinct banks), and each lane reads back what the matrix-core
-// layout gives it: the header (d, dmin, scales) and slice c of each 32-byte qs chunk (Q5K also
-// qh bytes 8c .. 8c + 7), into d[0..3], d[4 + 2k..5 + 2k] (chunk k) and d[12..13].
+// rows (row q = lane / 4, the unit's 16-byte pieces, piece p at slot p ^ ((q >> 2) & 3) of a
+// 192-byte row: the quads' 64-byte writes and the 16 rows' reads of one piece fall on
+// distinct banks), and each lane reads back what the matrix-core layout gives it: the header
+// (d, dmin, scales) and slice c of each 32-byte qs chunk (Q5K also qh bytes 8c .. 8c + 7),
+// into d[0..3], d[4 + 2k..5 + 2k] (chunk k) and d[12..13].
+constexpr uint32_t MM_WT = 192;  // LDS bytes a row of a K-quant unit
 template <uint32_t TY>
 __device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>], uint8_t* wt, uint32_t c, uint32_t rl) {
     if constexpr (TY == G_Q4K || TY == G_Q5K) {
-        constexpr uint32_t UB = MM_UB<TY>, NP = UB / 16, QS = TY == G_Q4K ? 16 : 48;
-        const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u;
+        constexpr uint32_t NP = MM_UB<TY> / 16, QP = TY == G_Q4K ? 1 : 3;  // pieces; first qs piece
+        const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u, fq = (q >> 2) & 3u;
 #pragma unroll
         for (int l = 0; l < 3; l++)
-            *(u32x4*)(wt + q * UB + 16 * min(4 * l + pq, NP - 1)) =
+            *(u32x4*)(wt + q * MM_WT + 16 * (min(4 * l + pq, NP - 1) ^ fq)) =
                 u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
-        const uint8_t* rw = wt + rl * UB;
-        const u32x4 h = *(const u32x4*)rw;
+        const uint8_t* rw = wt + rl * MM_WT;
+        const uint32_t fr = (rl >> 2) & 3u;
+        const u32x4 h = *(const u32x4*)(rw + 16 * fr);
         d[0] = h[0]; d[1] = h[1]; d[2] = h[2]; d[3] = h[3];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const u32x2 v = *(const u32x2*)(rw + QS + 32 * k + 8 * c);
+            const u32x2 v = *(const u32x2*)(rw + 16 * ((QP + 2 * k + (c >> 1)) ^ fr) + 8 * (c & 1));
             d[4 + 2 * k] = v[0];
             d[5 + 2 * k] = v[1];
         }
         if constexpr (TY == G_Q5K) {
-            const u32x2 v = *(const u32x2*)(rw + 16 + 8 * c);
+            const u32x2 v = *(const u32x2*)(rw + 16 * ((1 + (c >> 1)) ^ fr) + 8 * (c & 1));
             d[12] = v[0];
             d[13] = v[1];
         }
@@ -714,7 +717,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
     __shared__ __attribute__((aligned(16))) f16 xs[16 * XS];
     __shared__ __attribute__((aligned(16))) float ss[SUM ? MM_K<TY> * 8 * 16 : 4];
     constexpr bool KQ = TY == G_Q4K || TY == G_Q5K;  // units pass through LDS (mm_fix)
-    __shared__ __attribute__((aligned(16))) uint8_t wtb[KQ ? W * 16 * MM_UB<TY> : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t wtb[KQ ? W * 16 * MM_WT : 16];
     __shared__ uint32_t last;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t c = lane >> 4, rl = lane & 15;
@@ -722,7 +725,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
     const bool live = r0 < p.rows;  // the wave has rows
     // the rows a lane loads: its matrix-core row, or (KQ) its lane quad's
     const uint8_t* rowp = p.w + (size_t)min(KQ ? r0 + (lane >> 2) : r, p.rows - 1) * p.row_bytes;
-    uint8_t* wt = wtb + (KQ ? w * 16 * MM_UB<TY> : 0);
+    uint8_t* wt = wtb + (KQ ? w * 16 * MM_WT : 0);
     const float fl = c >= 2 ? 1.0f / MM_LO : 1.0f;
     const uint32_t kz0 = p.par ? blockIdx.z : 0, kz1 = p.par ? blockIdx.z + 1 : p.ks;
     float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
