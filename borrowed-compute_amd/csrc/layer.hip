@@ -559,8 +559,8 @@ __device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>], uint8_t* wt, uint3
         const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u, fq = (q >> 2) & 3u;
 #pragma unroll
         for (int l = 0; l < 3; l++)
-            *(u32x4*)(wt + q * MM_WT + 16 * (min(4 * l + pq, NP - 1) ^ fq)) =
-                u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
+            if (4 * l + pq < NP)  // (the last load's repeats of the unit's last piece stay out)
+                *(u32x4*)(wt + q * MM_WT + 16 * ((4 * l + pq) ^ fq)) = u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
         const uint8_t* rw = wt + rl * MM_WT;
         const uint32_t fr = (rl >> 2) & 3u;
         const u32x4 h = *(const u32x4*)(rw + 16 * fr);
@@ -796,7 +796,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                             accb = __builtin_amdgcn_mfma_f32_16x16x4f32(s0, m.b0, accb, 0, 0, 0);
                             accb = __builtin_amdgcn_mfma_f32_16x16x4f32(s1, m.b1, accb, 0, 0, 0);
                         }
-                        f32x4 accu = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                        f32x4 accu = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, accu2 = accu;  // even, odd groups
 #pragma unroll
                         for (int j = 0; j < 8; j++) {
                             const uint32_t col = lu * 256 + 32 * j;
@@ -806,7 +806,8 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                             mm_group<TY>(pk[f], m, ub, j, c, fl, q, q4, a0, a1);
                             if constexpr (TY == G_Q4K || TY == G_Q5K) {
                                 const half8 xa = *(const half8*)&xs[rl * XS + col + 8 * c];
-                                accu = mfma16(xa, q, accu);
+                                if (j % 2 == 0) accu = mfma16(xa, q, accu);
+                                else accu2 = mfma16(xa, q, accu2);
                             } else if constexpr (TY == G_F16) {
                                 const half8 xa = *(const half8*)&xs[rl * XS + col + 8 * c];
                                 acc = mfma16(xa, q, acc);
@@ -827,7 +828,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                         }
                         if constexpr (TY == G_Q4K || TY == G_Q5K) {
 #pragma unroll
-                            for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(m.dl, accu[i], acc[i]);
+                            for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(m.dl, accu[i] + accu2[i], acc[i]);
                         }
                     }
                     // the unit's registers are free: load into them directly (a load hoisted
