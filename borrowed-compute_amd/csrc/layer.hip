@@ -387,7 +387,9 @@ constexpr uint32_t MM_MIN = 8;     // batches of at least this many rows take th
 // LDS (the 8: 16-byte reads of 16 rows on distinct banks); the K-quants also pass each unit's
 // bytes through LDS, so their splits are shorter.
 template <uint32_t TY>
-constexpr uint32_t MM_K = TY == G_Q4K || TY == G_Q5K ? 4 : 8;
+constexpr bool MM_LDSP = TY == G_Q4K || TY == G_Q5K || TY == G_Q8_0;  // units pass through LDS
+template <uint32_t TY>
+constexpr uint32_t MM_K = MM_LDSP<TY> ? 4 : 8;
 template <uint32_t TY>
 constexpr uint32_t MM_XS = MM_K<TY> * 256 + 8;
 constexpr uint32_t MM_PAR = MATMUL_COUNTERS;  // tiles (W x 16 rows x 8 inputs) up to which K splits run in parallel
@@ -404,13 +406,13 @@ constexpr bool mm_sum() {
 }
 // Dwords a lane holds of one unit (8 groups) of its row.
 template <uint32_t TY>
-constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 32 : TY == G_Q4_0 ? 32 : TY == G_Q4_1 ? 24
+constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 20 : TY == G_Q4_0 ? 32 : TY == G_Q4_1 ? 24
                  : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 14 : 29;
 // Units loaded ahead; waves a workgroup (eight where the registers allow four waves a SIMD).
 template <uint32_t TY>
 constexpr int MM_PF = 2;
 template <uint32_t TY>
-constexpr int MM_W = MW<TY> <= 16 ? 8 : 4;
+constexpr int MM_W = MM_LDSP<TY> ? 8 : 4;
 // Bytes of a unit.
 template <uint32_t TY>
 constexpr uint32_t MM_UB = TY == G_F16 ? 512 : TY == G_Q8_0 ? 272 : TY == G_Q4_0 ? 144 : TY == G_Q4_1 ? 160
@@ -488,12 +490,21 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
             const u32x4 v = *(const u32x4*)(row + (size_t)(8 * u + j) * 64 + 16 * c);
             d[4 * j] = v[0]; d[4 * j + 1] = v[1]; d[4 * j + 2] = v[2]; d[4 * j + 3] = v[3];
         }
-    } else if constexpr (TY == G_Q8_0 || TY == G_Q4_0) {
-        constexpr uint32_t BS = TY == G_Q8_0 ? 34 : 18;
+    } else if constexpr (TY == G_Q8_0) {
+        // Row-contiguous lane order as the K-quants' (below): 17 pieces a unit, lane quad q
+        // takes pieces 4 l + (lane & 3), l < 5 (the repeats past the unit are its last piece).
+        const uint8_t* bb = row + (size_t)u * 272;
+        const uint32_t pq = threadIdx.x & 3u;
+#pragma unroll
+        for (int l = 0; l < 5; l++) {
+            const u32x4 v = *(const u32x4*)(bb + 16 * min(4 * l + pq, 16u));
+            d[4 * l] = v[0]; d[4 * l + 1] = v[1]; d[4 * l + 2] = v[2]; d[4 * l + 3] = v[3];
+        }
+    } else if constexpr (TY == G_Q4_0) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const uint8_t* bb = row + (size_t)(8 * u + j) * BS;
-            ld3(bb + 2 + (TY == G_Q8_0 ? 8 * c : 8 * (c & 1)), &d[4 * j]);
+            const uint8_t* bb = row + (size_t)(8 * u + j) * 18;
+            ld3(bb + 2 + 8 * (c & 1), &d[4 * j]);
             d[4 * j + 3] = ld16(bb);
         }
     } else if constexpr (TY == G_Q5_0) {
@@ -551,17 +562,27 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
 // distinct banks), and each lane reads back what the matrix-core layout gives it: the header
 // (d, dmin, scales) and slice c of each 32-byte qs chunk (Q5K also qh bytes 8c .. 8c + 7),
 // into d[0..3], d[4 + 2k..5 + 2k] (chunk k) and d[12..13].
-constexpr uint32_t MM_WT = 192;  // LDS bytes a row of a K-quant unit
+// LDS bytes a row of a unit: K-quants 192 (swizzled pieces), Q8_0 272 (the unit as it is:
+// a stride of 68 dwords puts the 16 rows' dword reads of one offset on distinct banks).
+template <uint32_t TY>
+constexpr uint32_t MM_WT = TY == G_Q8_0 ? 272 : 192;
 template <uint32_t TY>
 __device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>], uint8_t* wt, uint32_t c, uint32_t rl) {
+    if constexpr (TY == G_Q8_0) {  // the unit to the LDS rows as it is; mm_group reads each group
+        const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u;
+#pragma unroll
+        for (int l = 0; l < 5; l++)
+            if (4 * l + pq < 17)
+                *(u32x4*)(wt + q * 272 + 16 * (4 * l + pq)) = u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
+    }
     if constexpr (TY == G_Q4K || TY == G_Q5K) {
         constexpr uint32_t NP = MM_UB<TY> / 16, QP = TY == G_Q4K ? 1 : 3;  // pieces; first qs piece
         const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u, fq = (q >> 2) & 3u;
 #pragma unroll
         for (int l = 0; l < 3; l++)
             if (4 * l + pq < NP)  // (the last load's repeats of the unit's last piece stay out)
-                *(u32x4*)(wt + q * MM_WT + 16 * ((4 * l + pq) ^ fq)) = u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
-        const uint8_t* rw = wt + rl * MM_WT;
+                *(u32x4*)(wt + q * MM_WT<TY> + 16 * ((4 * l + pq) ^ fq)) = u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
+        const uint8_t* rw = wt + rl * MM_WT<TY>;
         const uint32_t fr = (rl >> 2) & 3u;
         const u32x4 h = *(const u32x4*)(rw + 16 * fr);
         d[0] = h[0]; d[1] = h[1]; d[2] = h[2]; d[3] = h[3];
@@ -611,16 +632,17 @@ __device__ __forceinline__ MMUnit mm_unit(const uint32_t (&d)[MW<TY>], uint32_t 
 // Q6K gives two half operands q4[0], q4[1] (16x16x16 MFMAs) and a0, a1.
 template <uint32_t TY>
 __device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const MMUnit& m, const uint8_t* unit_base,
-                                         int j, uint32_t c, float fl, half8& q, half4 (&q4)[2], float& a0,
-                                         float& a1) {
+                                         const uint8_t* rw, int j, uint32_t c, float fl, half8& q, half4 (&q4)[2],
+                                         float& a0, float& a1) {
     if constexpr (TY == G_F16) {  // weights 8c .. 8c + 7 in order (x staged unpermuted)
         q = __builtin_bit_cast(half8, u32x4{d[4 * j], d[4 * j + 1], d[4 * j + 2], d[4 * j + 3]});
-    } else if constexpr (TY == G_Q8_0) {
-        const uint8_t* p = unit_base + 34 * j + 2 + 8 * c;
-        uint32_t w0, w1;
-        align8(p, &d[4 * j], w0, w1);
+    } else if constexpr (TY == G_Q8_0) {  // from the lane's LDS row rw (the unit, 16-aligned)
+        const uint32_t b = 34 * j + 2 + 8 * c, a = b & ~3u, sh = b & 3u;  // qs bytes 8c .. of block j
+        const uint32_t w[3] = {*(const uint32_t*)(rw + a), *(const uint32_t*)(rw + a + 4),
+                               *(const uint32_t*)(rw + a + 4 + 2 * sh)};
+        const uint32_t w0 = __builtin_amdgcn_alignbyte(w[1], w[0], sh), w1 = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
         q = bytes8_f16(w0 ^ 0x80808080u, w1 ^ 0x80808080u, half2{(f16)1152.0f, (f16)1152.0f});
-        a0 = h2f(d[4 * j + 3]) * fl;
+        a0 = h2f(*(const uint16_t*)(rw + 34 * j)) * fl;
     } else if constexpr (TY == G_Q4_0) {
         // lanes 0, 1: low nibbles, lanes 2, 3: high nibbles (weights 16 ..), as q - 8
         const uint8_t* p = unit_base + 18 * j + 2 + 8 * (c & 1);
@@ -716,8 +738,8 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
     constexpr uint32_t XS = MM_XS<TY>;
     __shared__ __attribute__((aligned(16))) f16 xs[16 * XS];
     __shared__ __attribute__((aligned(16))) float ss[SUM ? MM_K<TY> * 8 * 16 : 4];
-    constexpr bool KQ = TY == G_Q4K || TY == G_Q5K;  // units pass through LDS (mm_fix)
-    __shared__ __attribute__((aligned(16))) uint8_t wtb[KQ ? W * 16 * MM_WT : 16];
+    constexpr bool KQ = MM_LDSP<TY>;  // units pass through LDS (mm_fix)
+    __shared__ __attribute__((aligned(16))) uint8_t wtb[KQ ? W * 16 * MM_WT<TY> : 16];
     __shared__ uint32_t last;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t c = lane >> 4, rl = lane & 15;
@@ -725,7 +747,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
     const bool live = r0 < p.rows;  // the wave has rows
     // the rows a lane loads: its matrix-core row, or (KQ) its lane quad's
     const uint8_t* rowp = p.w + (size_t)min(KQ ? r0 + (lane >> 2) : r, p.rows - 1) * p.row_bytes;
-    uint8_t* wt = wtb + (KQ ? w * 16 * MM_WT : 0);
+    uint8_t* wt = wtb + (KQ ? w * 16 * MM_WT<TY> : 0);
     const float fl = c >= 2 ? 1.0f / MM_LO : 1.0f;
     const uint32_t kz0 = p.par ? blockIdx.z : 0, kz1 = p.par ? blockIdx.z + 1 : p.ks;
     float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -803,7 +825,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                             half8 q;
                             half4 q4[2];
                             float a0 = 0.0f, a1 = 0.0f;
-                            mm_group<TY>(pk[f], m, ub, j, c, fl, q, q4, a0, a1);
+                            mm_group<TY>(pk[f], m, ub, wt + rl * MM_WT<TY>, j, c, fl, q, q4, a0, a1);
                             if constexpr (TY == G_Q4K || TY == G_Q5K) {
                                 const half8 xa = *(const half8*)&xs[rl * XS + col + 8 * c];
                                 if (j % 2 == 0) accu = mfma16(xa, q, accu);
@@ -912,17 +934,13 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
 
 // Rows a workgroup of the format takes.
 static uint32_t mm_rows(uint32_t type) {
-    switch (type) {
-        case G_Q4K: return 16 * MM_W<G_Q4K>;
-        case G_Q5K: return 16 * MM_W<G_Q5K>;
-        default: return 64;  // MW > 16: four waves
-    }
+    return type == G_Q4K || type == G_Q5K || type == G_Q8_0 ? 16 * MM_W<G_Q4K> : 16 * MM_W<G_F16>;
 }
 // K splits of a product: about two workgroups a CU from the rows alone (never from n), each
 // split at most MM_K units.
 static uint32_t mm_ks(uint32_t type, uint32_t rows, uint32_t cols) {
     const uint32_t rt = (rows + mm_rows(type) - 1) / mm_rows(type), units = cols / 256;
-    const uint32_t kmax = type == G_Q4K || type == G_Q5K ? MM_K<G_Q4K> : MM_K<G_Q8_0>;
+    const uint32_t kmax = type == G_Q4K || type == G_Q5K || type == G_Q8_0 ? MM_K<G_Q4K> : MM_K<G_F16>;
     uint32_t ks = max(512u / rt, 1u);
     ks = max(ks, (units + kmax - 1) / kmax);
     ks = min(ks, units);
