@@ -387,7 +387,7 @@ constexpr uint32_t MM_MIN = 8;     // batches of at least this many rows take th
 // LDS (the 8: 16-byte reads of 16 rows on distinct banks); the K-quants also pass each unit's
 // bytes through LDS, so their splits are shorter.
 template <uint32_t TY>
-constexpr bool MM_LDSP = TY == G_Q4K || TY == G_Q5K || TY == G_Q8_0;  // units pass through LDS
+constexpr bool MM_LDSP = TY == G_Q4K || TY == G_Q5K || TY == G_Q8_0 || TY == G_Q6K;  // units pass through LDS
 template <uint32_t TY>
 constexpr uint32_t MM_K = MM_LDSP<TY> ? 4 : 8;
 template <uint32_t TY>
@@ -404,10 +404,12 @@ template <uint32_t TY>
 constexpr bool mm_sum() {
     return TY == G_Q4_1 || TY == G_Q5_1 || TY == G_Q4K || TY == G_Q5K;
 }
-// Dwords a lane holds of one unit (8 groups) of its row.
+// Dwords a lane loads of one unit (8 groups) of its row, and holds of it after mm_fix.
 template <uint32_t TY>
 constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 20 : TY == G_Q4_0 ? 32 : TY == G_Q4_1 ? 24
-                 : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 14 : 29;
+                 : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 12 : 16;
+template <uint32_t TY>
+constexpr int MWD = TY == G_Q5K ? 14 : TY == G_Q6K ? 29 : MW<TY>;
 // Units loaded ahead; waves a workgroup (eight where the registers allow four waves a SIMD).
 template <uint32_t TY>
 constexpr int MM_PF = 2;
@@ -538,21 +540,18 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
             const u32x4 v = *(const u32x4*)(bb + 16 * min(4 * l + pq, NP - 1));
             d[4 * l] = v[0]; d[4 * l + 1] = v[1]; d[4 * l + 2] = v[2]; d[4 * l + 3] = v[3];
         }
-    } else {  // Q6K: lane c's weights 4c .. 4c + 3 and 16 + 4c .. of each 32-weight run
+    } else {  // Q6K, row-contiguous lane order: the 16-byte pieces from the unit's start
+        // rounded down to 16 (at most 14 pieces hold its 210 bytes; a lane quad takes pieces
+        // 4 l + (lane & 3), l < 4, those past the last that holds unit bytes repeat it, so no
+        // read leaves the 16-byte blocks the unit touches)
         const uint8_t* bb = row + (size_t)u * 210;
-        const uintptr_t a = (uintptr_t)bb & ~(uintptr_t)3;
-        // ql runs 0..3 (64 hh + 32 s), qh runs 0..1 (128 + 32 hh): dwords at 4c and 16 + 4c of
-        // the run (two each, from the aligned base); then scales and d (bytes 192..209)
+        const uintptr_t a0 = (uintptr_t)bb & ~(uintptr_t)15;
+        const uint32_t km = (uint32_t)((uintptr_t)bb + 209 - a0) / 16, pq = threadIdx.x & 3u;
 #pragma unroll
-        for (int k = 0; k < 6; k++) {
-            const uint32_t o = k < 4 ? 32 * k : 128 + 32 * (k - 4);
-            d[4 * k] = *(const uint32_t*)(a + o + 4 * c);
-            d[4 * k + 1] = *(const uint32_t*)(a + o + 4 * c + 4);
-            d[4 * k + 2] = *(const uint32_t*)(a + o + 16 + 4 * c);
-            d[4 * k + 3] = *(const uint32_t*)(a + o + 20 + 4 * c);
+        for (int l = 0; l < 4; l++) {
+            const u32x4 v = *(const u32x4*)(a0 + 16 * min(4 * l + pq, km));
+            d[4 * l] = v[0]; d[4 * l + 1] = v[1]; d[4 * l + 2] = v[2]; d[4 * l + 3] = v[3];
         }
-#pragma unroll
-        for (int k = 0; k < 5; k++) d[24 + k] = *(const uint32_t*)(a + 192 + 4 * k);
     }
 }
 
@@ -565,15 +564,44 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
 // LDS bytes a row of a unit: K-quants 192 (swizzled pieces), Q8_0 272 (the unit as it is:
 // a stride of 68 dwords puts the 16 rows' dword reads of one offset on distinct banks).
 template <uint32_t TY>
-constexpr uint32_t MM_WT = TY == G_Q8_0 ? 272 : 192;
+constexpr uint32_t MM_WT = TY == G_Q8_0 ? 272 : TY == G_Q6K ? 240 : 192;
+// s: the lane's loads; d: what mm_unit and mm_group read; sq, sm: the lane quad's and the
+// lane's own row's unit start modulo 16 (Q6K).
 template <uint32_t TY>
-__device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>], uint8_t* wt, uint32_t c, uint32_t rl) {
+__device__ __forceinline__ void mm_fix(const uint32_t (&s)[MW<TY>], uint32_t (&d)[MWD<TY>], uint8_t* wt, uint32_t c,
+                                       uint32_t rl, uint32_t sq, uint32_t sm) {
+    if constexpr (!MM_LDSP<TY> || TY == G_Q8_0) {
+#pragma unroll
+        for (int k = 0; k < MW<TY>; k++) d[k] = s[k];
+    }
     if constexpr (TY == G_Q8_0) {  // the unit to the LDS rows as it is; mm_group reads each group
         const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u;
 #pragma unroll
         for (int l = 0; l < 5; l++)
             if (4 * l + pq < 17)
-                *(u32x4*)(wt + q * 272 + 16 * (4 * l + pq)) = u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
+                *(u32x4*)(wt + q * 272 + 16 * (4 * l + pq)) = u32x4{s[4 * l], s[4 * l + 1], s[4 * l + 2], s[4 * l + 3]};
+    }
+    if constexpr (TY == G_Q6K) {
+        // pieces to the LDS rows as loaded (unit byte b at sq + b of the quad's row); then the
+        // lane reads, from its own row (byte b at sm + b), the dwords the unpacking takes: at 4c
+        // and 16 + 4c (two each) of the six 32-byte ql / qh runs, and bytes 192..209 (scales, d),
+        // all from the dword-aligned base of the unit's start
+        const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u, kq = (sq + 209) / 16;
+#pragma unroll
+        for (int l = 0; l < 4; l++)
+            if (4 * l + pq <= kq)
+                *(u32x4*)(wt + q * 240 + 16 * (4 * l + pq)) = u32x4{s[4 * l], s[4 * l + 1], s[4 * l + 2], s[4 * l + 3]};
+        const uint8_t* a = wt + rl * 240 + (sm & ~3u);
+#pragma unroll
+        for (int k = 0; k < 6; k++) {
+            const uint32_t o = k < 4 ? 32 * k : 128 + 32 * (k - 4);
+            d[4 * k] = *(const uint32_t*)(a + o + 4 * c);
+            d[4 * k + 1] = *(const uint32_t*)(a + o + 4 * c + 4);
+            d[4 * k + 2] = *(const uint32_t*)(a + o + 16 + 4 * c);
+            d[4 * k + 3] = *(const uint32_t*)(a + o + 20 + 4 * c);
+        }
+#pragma unroll
+        for (int k = 0; k < 5; k++) d[24 + k] = *(const uint32_t*)(a + 192 + 4 * k);
     }
     if constexpr (TY == G_Q4K || TY == G_Q5K) {
         constexpr uint32_t NP = MM_UB<TY> / 16, QP = TY == G_Q4K ? 1 : 3;  // pieces; first qs piece
@@ -581,7 +609,7 @@ __device__ __forceinline__ void mm_fix(uint32_t (&d)[MW<TY>], uint8_t* wt, uint3
 #pragma unroll
         for (int l = 0; l < 3; l++)
             if (4 * l + pq < NP)  // (the last load's repeats of the unit's last piece stay out)
-                *(u32x4*)(wt + q * MM_WT<TY> + 16 * ((4 * l + pq) ^ fq)) = u32x4{d[4 * l], d[4 * l + 1], d[4 * l + 2], d[4 * l + 3]};
+                *(u32x4*)(wt + q * MM_WT<TY> + 16 * ((4 * l + pq) ^ fq)) = u32x4{s[4 * l], s[4 * l + 1], s[4 * l + 2], s[4 * l + 3]};
         const uint8_t* rw = wt + rl * MM_WT<TY>;
         const uint32_t fr = (rl >> 2) & 3u;
         const u32x4 h = *(const u32x4*)(rw + 16 * fr);
@@ -608,7 +636,7 @@ struct MMUnit {
 };
 
 template <uint32_t TY>
-__device__ __forceinline__ MMUnit mm_unit(const uint32_t (&d)[MW<TY>], uint32_t c, float fl) {
+__device__ __forceinline__ MMUnit mm_unit(const uint32_t (&d)[MWD<TY>], uint32_t c, float fl) {
     MMUnit m;
     if constexpr (TY == G_Q4K || TY == G_Q5K) {
         // scale and min bytes of sub-blocks 0..3 and 4..7 (6 bits each, quant.rs:136-146)
@@ -631,7 +659,7 @@ __device__ __forceinline__ MMUnit mm_unit(const uint32_t (&d)[MW<TY>], uint32_t 
 // Group j of a loaded unit for lane c: B operand(s) and a (fl and the field scale folded in).
 // Q6K gives two half operands q4[0], q4[1] (16x16x16 MFMAs) and a0, a1.
 template <uint32_t TY>
-__device__ __forceinline__ void mm_group(const uint32_t (&d)[MW<TY>], const MMUnit& m, const uint8_t* unit_base,
+__device__ __forceinline__ void mm_group(const uint32_t (&d)[MWD<TY>], const MMUnit& m, const uint8_t* unit_base,
                                          const uint8_t* rw, int j, uint32_t c, float fl, half8& q, half4 (&q4)[2],
                                          float& a0, float& a1) {
     if constexpr (TY == G_F16) {  // weights 8c .. 8c + 7 in order (x staged unpermuted)
@@ -745,8 +773,9 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
     const uint32_t c = lane >> 4, rl = lane & 15;
     const uint32_t r0 = blockIdx.x * (16 * W) + 16 * w, r = r0 + rl, i0 = blockIdx.y * 8;
     const bool live = r0 < p.rows;  // the wave has rows
-    // the rows a lane loads: its matrix-core row, or (KQ) its lane quad's
-    const uint8_t* rowp = p.w + (size_t)min(KQ ? r0 + (lane >> 2) : r, p.rows - 1) * p.row_bytes;
+    // the rows a lane loads: its matrix-core row (mrowp), or (KQ) its lane quad's
+    const uint8_t* mrowp = p.w + (size_t)min(r, p.rows - 1) * p.row_bytes;
+    const uint8_t* rowp = KQ ? p.w + (size_t)min(r0 + (lane >> 2), p.rows - 1) * p.row_bytes : mrowp;
     uint8_t* wt = wtb + (KQ ? w * 16 * MM_WT<TY> : 0);
     const float fl = c >= 2 ? 1.0f / MM_LO : 1.0f;
     const uint32_t kz0 = p.par ? blockIdx.z : 0, kz1 = p.par ? blockIdx.z + 1 : p.ks;
@@ -810,9 +839,11 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                 for (int f = 0; f < PF; f++) {
                     const uint32_t lu = u0 + f;
                     if (lu < nu) {
-                        const uint8_t* ub = rowp + (size_t)(ua + lu) * MM_UB<TY>;
-                        mm_fix<TY>(pk[f], wt, c, rl);
-                        const MMUnit m = mm_unit<TY>(pk[f], c, fl);
+                        const uint8_t* ub = mrowp + (size_t)(ua + lu) * MM_UB<TY>;  // the lane's row's unit
+                        const uint8_t* qb = rowp + (size_t)(ua + lu) * MM_UB<TY>;   // its lane quad's
+                        uint32_t dd[MWD<TY>];
+                        mm_fix<TY>(pk[f], dd, wt, c, rl, (uint32_t)((uintptr_t)qb & 15u), (uint32_t)((uintptr_t)ub & 15u));
+                        const MMUnit m = mm_unit<TY>(dd, c, fl);
                         if constexpr (SUM) {  // sum_g b_g s_g over the unit's groups, 4 at a time
                             const float s0 = ss[(lu * 8 + c) * 16 + rl], s1 = ss[(lu * 8 + 4 + c) * 16 + rl];
                             accb = __builtin_amdgcn_mfma_f32_16x16x4f32(s0, m.b0, accb, 0, 0, 0);
@@ -825,7 +856,7 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
                             half8 q;
                             half4 q4[2];
                             float a0 = 0.0f, a1 = 0.0f;
-                            mm_group<TY>(pk[f], m, ub, wt + rl * MM_WT<TY>, j, c, fl, q, q4, a0, a1);
+                            mm_group<TY>(dd, m, ub, wt + rl * MM_WT<TY>, j, c, fl, q, q4, a0, a1);
                             if constexpr (TY == G_Q4K || TY == G_Q5K) {
                                 const half8 xa = *(const half8*)&xs[rl * XS + col + 8 * c];
                                 if (j % 2 == 0) accu = mfma16(xa, q, accu);
@@ -934,13 +965,13 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
 
 // Rows a workgroup of the format takes.
 static uint32_t mm_rows(uint32_t type) {
-    return type == G_Q4K || type == G_Q5K || type == G_Q8_0 ? 16 * MM_W<G_Q4K> : 16 * MM_W<G_F16>;
+    return type == G_Q4K || type == G_Q5K || type == G_Q8_0 || type == G_Q6K ? 16 * MM_W<G_Q4K> : 16 * MM_W<G_F16>;
 }
 // K splits of a product: about two workgroups a CU from the rows alone (never from n), each
 // split at most MM_K units.
 static uint32_t mm_ks(uint32_t type, uint32_t rows, uint32_t cols) {
     const uint32_t rt = (rows + mm_rows(type) - 1) / mm_rows(type), units = cols / 256;
-    const uint32_t kmax = type == G_Q4K || type == G_Q5K || type == G_Q8_0 ? MM_K<G_Q4K> : MM_K<G_F16>;
+    const uint32_t kmax = type == G_Q4K || type == G_Q5K || type == G_Q8_0 || type == G_Q6K ? MM_K<G_Q4K> : MM_K<G_F16>;
     uint32_t ks = max(512u / rt, 1u);
     ks = max(ks, (units + kmax - 1) / kmax);
     ks = min(ks, units);
