@@ -387,7 +387,7 @@ constexpr uint32_t MM_MIN = 8;     // batches of at least this many rows take th
 // LDS (the 8: 16-byte reads of 16 rows on distinct banks); the K-quants also pass each unit's
 // bytes through LDS, so their splits are shorter.
 template <uint32_t TY>
-constexpr bool MM_LDSP = TY == G_Q4K || TY == G_Q5K || TY == G_Q8_0 || TY == G_Q6K;  // units pass through LDS
+constexpr bool MM_LDSP = TY != G_F16;  // units pass through LDS (all block formats)
 template <uint32_t TY>
 constexpr uint32_t MM_K = MM_LDSP<TY> ? 4 : 8;
 template <uint32_t TY>
@@ -406,8 +406,7 @@ constexpr bool mm_sum() {
 }
 // Dwords a lane loads of one unit (8 groups) of its row, and holds of it after mm_fix.
 template <uint32_t TY>
-constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 20 : TY == G_Q4_0 ? 32 : TY == G_Q4_1 ? 24
-                 : TY == G_Q5_0 ? 40 : TY == G_Q5_1 ? 32 : TY == G_Q4K ? 12 : TY == G_Q5K ? 12 : 16;
+constexpr int MW = TY == G_F16 ? 32 : TY == G_Q8_0 ? 20 : TY == G_Q6K ? 16 : 12;
 template <uint32_t TY>
 constexpr int MWD = TY == G_Q5K ? 14 : TY == G_Q6K ? 29 : MW<TY>;
 // Units loaded ahead; waves a workgroup (eight where the registers allow four waves a SIMD).
@@ -462,26 +461,6 @@ __device__ __forceinline__ half8 fields8(uint32_t v0, uint32_t v1, uint32_t m, h
 }
 // Four bits to bit 4 of bytes 0..3.
 __device__ __forceinline__ uint32_t bit4_spread(uint32_t b4) { return ((b4 * 0x00204081u) & 0x01010101u) << 4; }
-// Eight bytes at a 2-byte-aligned p from the three dwords loaded at p & ~3 (`ld3`).
-__device__ __forceinline__ void ld3(const uint8_t* p, uint32_t* d) {
-    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
-    const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
-    d[0] = *(const uint32_t*)a;
-    d[1] = *(const uint32_t*)(a + 4);
-    // the third dword only holds bytes of p's eight when sh = 2; otherwise the second again,
-    // so that no read touches a dword past the eight bytes' last
-    d[2] = *(const uint32_t*)(a + 4 + 2 * sh);
-}
-__device__ __forceinline__ void align8(const uint8_t* p, const uint32_t* d, uint32_t& w0, uint32_t& w1) {
-    const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
-    w0 = __builtin_amdgcn_alignbyte(d[1], d[0], sh);
-    w1 = __builtin_amdgcn_alignbyte(d[2], d[1], sh);
-}
-// v[c] for the lane's c < 4.
-__device__ __forceinline__ uint32_t pick4(uint32_t c, uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3) {
-    return c < 2 ? (c == 0 ? v0 : v1) : (c == 2 ? v2 : v3);
-}
-
 // Lane (c, row) loads of unit u (8 groups) of its row.
 template <uint32_t TY>
 __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_t u, uint32_t c,
@@ -502,30 +481,15 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
             const u32x4 v = *(const u32x4*)(bb + 16 * min(4 * l + pq, 16u));
             d[4 * l] = v[0]; d[4 * l + 1] = v[1]; d[4 * l + 2] = v[2]; d[4 * l + 3] = v[3];
         }
-    } else if constexpr (TY == G_Q4_0) {
+    } else if constexpr (TY == G_Q4_0 || TY == G_Q4_1 || TY == G_Q5_0 || TY == G_Q5_1) {
+        // row-contiguous lane order, as the K-quants' below (9 to 12 pieces a unit)
+        constexpr uint32_t NP = MM_UB<TY> / 16;
+        const uint8_t* bb = row + (size_t)u * MM_UB<TY>;
+        const uint32_t pq = threadIdx.x & 3u;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint8_t* bb = row + (size_t)(8 * u + j) * 18;
-            ld3(bb + 2 + 8 * (c & 1), &d[4 * j]);
-            d[4 * j + 3] = ld16(bb);
-        }
-    } else if constexpr (TY == G_Q5_0) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint8_t* bb = row + (size_t)(8 * u + j) * 22;
-            ld3(bb + 6 + 8 * (c & 1), &d[5 * j]);
-            d[5 * j + 3] = ld16(bb);
-            d[5 * j + 4] = ld16(bb + 2 + 2 * (c >> 1));  // qh bytes 2 (c / 2), 2 (c / 2) + 1
-        }
-    } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
-        constexpr uint32_t BS = TY == G_Q4_1 ? 20 : 24, QS = TY == G_Q4_1 ? 4 : 8, N = MW<TY> / 8;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint8_t* bb = row + (size_t)(8 * u + j) * BS;
-            d[N * j] = ld32(bb + QS + 8 * (c & 1));
-            d[N * j + 1] = ld32(bb + QS + 8 * (c & 1) + 4);
-            d[N * j + 2] = ld32(bb);  // d, m
-            if constexpr (TY == G_Q5_1) d[N * j + 3] = ld32(bb + 4);  // qh
+        for (int l = 0; l < 3; l++) {
+            const u32x4 v = *(const u32x4*)(bb + 16 * min(4 * l + pq, NP - 1));
+            d[4 * l] = v[0]; d[4 * l + 1] = v[1]; d[4 * l + 2] = v[2]; d[4 * l + 3] = v[3];
         }
     } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
         // Row-contiguous lane order (the memory path coalesces consecutive lanes: 64 bytes of
@@ -563,23 +527,34 @@ __device__ __forceinline__ void mm_load(const uint8_t* __restrict__ row, uint32_
 // into d[0..3], d[4 + 2k..5 + 2k] (chunk k) and d[12..13].
 // LDS bytes a row of a unit: K-quants 192 (swizzled pieces), Q8_0 272 (the unit as it is:
 // a stride of 68 dwords puts the 16 rows' dword reads of one offset on distinct banks).
+// The 32-weight formats' units keep their bytes as they are, in rows of an odd number of
+// 16-byte pieces (Q4_1, Q5_1 padded by one) for the same bank spread.
 template <uint32_t TY>
-constexpr uint32_t MM_WT = TY == G_Q8_0 ? 272 : TY == G_Q6K ? 240 : 192;
+constexpr uint32_t MM_WT = TY == G_Q8_0 ? 272 : TY == G_Q6K ? 240 : TY == G_Q4_0 ? 144 : TY == G_Q4_1 ? 176
+                         : TY == G_Q5_0 ? 176 : TY == G_Q5_1 ? 208 : 192;
 // s: the lane's loads; d: what mm_unit and mm_group read; sq, sm: the lane quad's and the
 // lane's own row's unit start modulo 16 (Q6K).
 template <uint32_t TY>
 __device__ __forceinline__ void mm_fix(const uint32_t (&s)[MW<TY>], uint32_t (&d)[MWD<TY>], uint8_t* wt, uint32_t c,
                                        uint32_t rl, uint32_t sq, uint32_t sm) {
-    if constexpr (!MM_LDSP<TY> || TY == G_Q8_0) {
+    if constexpr (!MM_LDSP<TY>) {
 #pragma unroll
         for (int k = 0; k < MW<TY>; k++) d[k] = s[k];
     }
-    if constexpr (TY == G_Q8_0) {  // the unit to the LDS rows as it is; mm_group reads each group
+    if constexpr (TY == G_Q8_0 || TY == G_Q4_0 || TY == G_Q4_1 || TY == G_Q5_0 || TY == G_Q5_1) {
+        // the unit to the LDS rows as it is; mm_group reads each group from there
+        constexpr uint32_t NP = MM_UB<TY> / 16;
         const uint32_t q = (threadIdx.x & 63u) >> 2, pq = threadIdx.x & 3u;
 #pragma unroll
-        for (int l = 0; l < 5; l++)
-            if (4 * l + pq < 17)
-                *(u32x4*)(wt + q * 272 + 16 * (4 * l + pq)) = u32x4{s[4 * l], s[4 * l + 1], s[4 * l + 2], s[4 * l + 3]};
+        for (int l = 0; l < MW<TY> / 4; l++)
+            if (4 * l + pq < NP)
+                *(u32x4*)(wt + q * MM_WT<TY> + 16 * (4 * l + pq)) = u32x4{s[4 * l], s[4 * l + 1], s[4 * l + 2], s[4 * l + 3]};
+        if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {  // m of groups c and 4 + c (the b terms)
+            constexpr uint32_t BS = TY == G_Q4_1 ? 20 : 24;
+            const uint8_t* rw = wt + rl * MM_WT<TY>;
+            d[0] = *(const uint16_t*)(rw + BS * c + 2);
+            d[1] = *(const uint16_t*)(rw + BS * (4 + c) + 2);
+        }
     }
     if constexpr (TY == G_Q6K) {
         // pieces to the LDS rows as loaded (unit byte b at sq + b of the quad's row); then the
@@ -649,9 +624,8 @@ __device__ __forceinline__ MMUnit mm_unit(const uint32_t (&d)[MWD<TY>], uint32_t
         m.b0 = ndm * (float)((mnA >> (8 * c)) & 255u);
         m.b1 = ndm * (float)((mnB >> (8 * c)) & 255u);
     } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {
-        constexpr int N = MW<TY> / 8;
-        m.b0 = h2f(pick4(c, d[2], d[N + 2], d[2 * N + 2], d[3 * N + 2]) >> 16);
-        m.b1 = h2f(pick4(c, d[4 * N + 2], d[5 * N + 2], d[6 * N + 2], d[7 * N + 2]) >> 16);
+        m.b0 = h2f(d[0]);
+        m.b1 = h2f(d[1]);
     }
     return m;
 }
@@ -671,35 +645,38 @@ __device__ __forceinline__ void mm_group(const uint32_t (&d)[MWD<TY>], const MMU
         const uint32_t w0 = __builtin_amdgcn_alignbyte(w[1], w[0], sh), w1 = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
         q = bytes8_f16(w0 ^ 0x80808080u, w1 ^ 0x80808080u, half2{(f16)1152.0f, (f16)1152.0f});
         a0 = h2f(*(const uint16_t*)(rw + 34 * j)) * fl;
-    } else if constexpr (TY == G_Q4_0) {
-        // lanes 0, 1: low nibbles, lanes 2, 3: high nibbles (weights 16 ..), as q - 8
-        const uint8_t* p = unit_base + 18 * j + 2 + 8 * (c & 1);
-        uint32_t w0, w1;
-        align8(p, &d[4 * j], w0, w1);
-        const uint32_t sh = c < 2 ? 0u : 4u;
-        q = fields8(w0 >> sh, w1 >> sh, 0x000f000fu, half2{(f16)1032.0f, (f16)1032.0f});
-        a0 = h2f(d[4 * j + 3]) * fl;
-    } else if constexpr (TY == G_Q5_0) {
-        const uint8_t* p = unit_base + 22 * j + 6 + 8 * (c & 1);
-        uint32_t w0, w1;
-        align8(p, &d[5 * j], w0, w1);
-        const uint32_t sh = c < 2 ? 0u : 4u;
-        const uint32_t qh = (d[5 * j + 4] >> (8 * (c & 1))) & 255u;  // qh byte c: bit 4 of weights 8c ..
-        w0 = ((w0 >> sh) & 0x0f0f0f0fu) | bit4_spread(qh & 15u);
-        w1 = ((w1 >> sh) & 0x0f0f0f0fu) | bit4_spread(qh >> 4);
-        q = bytes8_f16(w0, w1, half2{(f16)1040.0f, (f16)1040.0f});
-        a0 = h2f(d[5 * j + 3]) * fl;
-    } else if constexpr (TY == G_Q4_1) {
-        const uint32_t sh = c < 2 ? 0u : 4u;
-        q = fields8(d[3 * j] >> sh, d[3 * j + 1] >> sh, 0x000f000fu, half2{(f16)1024.0f, (f16)1024.0f});
-        a0 = h2f(d[3 * j + 2] & 0xffffu) * fl;
-    } else if constexpr (TY == G_Q5_1) {
-        const uint32_t sh = c < 2 ? 0u : 4u;
-        const uint32_t qh = (d[4 * j + 3] >> (8 * c)) & 255u;  // qh byte c
-        const uint32_t w0 = ((d[4 * j] >> sh) & 0x0f0f0f0fu) | bit4_spread(qh & 15u);
-        const uint32_t w1 = ((d[4 * j + 1] >> sh) & 0x0f0f0f0fu) | bit4_spread(qh >> 4);
-        q = bytes8_f16(w0, w1, half2{(f16)1024.0f, (f16)1024.0f});
-        a0 = h2f(d[4 * j + 2] & 0xffffu) * fl;
+    } else if constexpr (TY == G_Q4_0 || TY == G_Q5_0) {
+        // from the lane's LDS row rw; lanes 0, 1: low nibbles, lanes 2, 3: high nibbles
+        // (weights 16 ..), as q - 8 (Q4_0) or, with qh byte c as bit 4, q - 16 (Q5_0)
+        constexpr uint32_t BS = TY == G_Q4_0 ? 18 : 22, QS = TY == G_Q4_0 ? 2 : 6;
+        const uint32_t b = BS * j + QS + 8 * (c & 1), a = b & ~3u, sh = b & 3u;
+        const uint32_t w[3] = {*(const uint32_t*)(rw + a), *(const uint32_t*)(rw + a + 4),
+                               *(const uint32_t*)(rw + a + 4 + 2 * sh)};
+        uint32_t w0 = __builtin_amdgcn_alignbyte(w[1], w[0], sh), w1 = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
+        const uint32_t ns = c < 2 ? 0u : 4u;
+        if constexpr (TY == G_Q4_0) {
+            q = fields8(w0 >> ns, w1 >> ns, 0x000f000fu, half2{(f16)1032.0f, (f16)1032.0f});
+        } else {
+            const uint32_t qh = *(const uint8_t*)(rw + BS * j + 2 + c);  // bit 4 of weights 8c ..
+            w0 = ((w0 >> ns) & 0x0f0f0f0fu) | bit4_spread(qh & 15u);
+            w1 = ((w1 >> ns) & 0x0f0f0f0fu) | bit4_spread(qh >> 4);
+            q = bytes8_f16(w0, w1, half2{(f16)1040.0f, (f16)1040.0f});
+        }
+        a0 = h2f(*(const uint16_t*)(rw + BS * j)) * fl;
+    } else if constexpr (TY == G_Q4_1 || TY == G_Q5_1) {  // from the lane's LDS row rw
+        constexpr uint32_t BS = TY == G_Q4_1 ? 20 : 24, QS = TY == G_Q4_1 ? 4 : 8;
+        const uint8_t* g = rw + BS * j;
+        const uint32_t x0 = *(const uint32_t*)(g + QS + 8 * (c & 1)), x1 = *(const uint32_t*)(g + QS + 8 * (c & 1) + 4);
+        const uint32_t ns = c < 2 ? 0u : 4u;
+        if constexpr (TY == G_Q4_1) {
+            q = fields8(x0 >> ns, x1 >> ns, 0x000f000fu, half2{(f16)1024.0f, (f16)1024.0f});
+        } else {
+            const uint32_t qh = g[4 + c];  // qh byte c
+            const uint32_t w0 = ((x0 >> ns) & 0x0f0f0f0fu) | bit4_spread(qh & 15u);
+            const uint32_t w1 = ((x1 >> ns) & 0x0f0f0f0fu) | bit4_spread(qh >> 4);
+            q = bytes8_f16(w0, w1, half2{(f16)1024.0f, (f16)1024.0f});
+        }
+        a0 = h2f(*(const uint16_t*)g) * fl;
     } else if constexpr (TY == G_Q4K || TY == G_Q5K) {
         const int k = j / 2, hi = j % 2;
         const uint32_t v0 = d[4 + 2 * k], v1 = d[5 + 2 * k];
@@ -965,13 +942,13 @@ __global__ __launch_bounds__(64 * MM_W<TY>, MM_W<TY> / 2) void k_matmul_mm(const
 
 // Rows a workgroup of the format takes.
 static uint32_t mm_rows(uint32_t type) {
-    return type == G_Q4K || type == G_Q5K || type == G_Q8_0 || type == G_Q6K ? 16 * MM_W<G_Q4K> : 16 * MM_W<G_F16>;
+    return type == G_F16 ? 16 * MM_W<G_F16> : 16 * MM_W<G_Q4K>;
 }
 // K splits of a product: about two workgroups a CU from the rows alone (never from n), each
 // split at most MM_K units.
 static uint32_t mm_ks(uint32_t type, uint32_t rows, uint32_t cols) {
     const uint32_t rt = (rows + mm_rows(type) - 1) / mm_rows(type), units = cols / 256;
-    const uint32_t kmax = type == G_Q4K || type == G_Q5K || type == G_Q8_0 || type == G_Q6K ? MM_K<G_Q4K> : MM_K<G_F16>;
+    const uint32_t kmax = type == G_F16 ? MM_K<G_F16> : MM_K<G_Q4K>;
     uint32_t ks = max(512u / rt, 1u);
     ks = max(ks, (units + kmax - 1) / kmax);
     ks = min(ks, units);
