@@ -111,7 +111,7 @@ hipError_t sample_launch(const float* scores, uint32_t rows, uint32_t vocab, flo
 bool ggml_block(uint32_t type, uint32_t& weights, uint32_t& bytes);
 // Input rows one product call takes: passes of 8 rows over the grid's y dimension (65535).
 constexpr uint32_t MATMUL_MAX_N = 8u * 65535u;
-// Batches of n >= 8 input rows of the quantised formats and F16 (cols a multiple of 256)
+// Batches of n >= 2 input rows of the quantised formats and F16 (cols a multiple of 256)
 // run on the matrix cores; their K splits may need matmul_scratch_bytes of scratch (partial
 // sums) and a context's MATMUL_COUNTERS arrival counters (zero when no product runs).
 constexpr uint32_t MATMUL_COUNTERS = 1024;

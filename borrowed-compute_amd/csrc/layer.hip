@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * MM_WAVES) void k_matmul(const MatmulParams p) 
 // last to finish (a device counter per tile) adds them: an input row's bits depend on that
 // row alone, never on n or its place in the batch.
 constexpr float MM_LO = 4096.0f;   // lo = (x - hi) * MM_LO
-constexpr uint32_t MM_MIN = 8;     // batches of at least this many rows take the matrix cores
+constexpr uint32_t MM_MIN = 2;     // batches of at least this many rows take the matrix cores (MM_FROM)
 // Units (256 columns) a K split at most: the staged x takes 16 rows x (256 MM_K + 8) halves of
 // LDS (the 8: 16-byte reads of 16 rows on distinct banks); the K-quants also pass each unit's
 // bytes through LDS, so their splits are shorter.

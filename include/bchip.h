@@ -232,11 +232,11 @@ int bchip_rope_append_attention_ragged(bchip_ctx* ctx, float* q, const float* k,
  * weight matrix as stored (rows of whole ggml blocks of `type`, row stride
  * cols / block_weights * block_bytes: matmul_rows passes its first `rows` rows only);
  * x [n][cols] and out [n][rows] f32. cols must be a multiple of 32 (256 for the K-quants);
- * w and x 16-byte aligned; n at most 524280 (8 x 65535) a call. Batches of 8 or more rows
- * of the block formats and F16 with cols a multiple of 256 run on the matrix cores (the
- * reference's batched product, gpu/mod.rs:33-41). An input row's result does not depend on
- * n among calls of fewer than 8 rows, nor among calls of 8 or more; between the two it
- * agrees within f32 rounding. Reruns give the same bits. */
+ * w and x 16-byte aligned; n at most 524280 (8 x 65535) a call. Batches of 2 or more rows
+ * of the block formats and F16 with cols a multiple of 256 run on the matrix cores, as the
+ * reference's do from MM_FROM = 2 rows (gpu/mod.rs:33-41). An input row's result does not
+ * depend on n or on its place among the batch's rows; a batch row agrees with the same row
+ * passed alone within f32 rounding (as the reference's). Reruns give the same bits. */
 int bchip_matmul(bchip_ctx* ctx, const void* w, uint32_t type, const float* x, float* out,
                  uint32_t rows, uint32_t cols, uint32_t n);
 

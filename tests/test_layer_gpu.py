@@ -1,8 +1,8 @@
 """The rest of a layer on the GPU against the oracle: the GGUF block-format product in
 every format (k_matmul, gpu/kernels.h:51-214, checked as Gpu::self_check checks it,
 gpu/mod.rs:181-206: within 1e-3 * (1 + |want|) of the f64 dequantized product), on the VALU
-for fewer than 8 input rows and on the matrix cores for batches of 8 or more (the
-reference's own batched product, gpu/mod.rs:33-41), its batch invariance and determinism
+for one input row and on the matrix cores for batches of 2 or more (the reference's own
+batched product from MM_FROM = 2 rows, gpu/mod.rs:33-41), its batch invariance and determinism
 (kernels.h:9-11), matmul_rows (gpu/mod.rs:163-178), RMSNorm (model.rs:381-388) and the
 elementwise ops (model.rs:337, 343, 371-377)."""
 import numpy as np
@@ -43,7 +43,7 @@ def within_selfcheck(got, want, what):
     assert (err <= bound).all(), f"{what}: got {got[worst]}, want {want[worst]} at {worst}"
 
 
-MM_TYPES = [O.F16, O.Q8_0, O.Q4_0, O.Q4_1, O.Q5_0, O.Q5_1, O.Q4K, O.Q5K, O.Q6K]  # matrix cores for n >= 8
+MM_TYPES = [O.F16, O.Q8_0, O.Q4_0, O.Q4_1, O.Q5_0, O.Q5_1, O.Q4K, O.Q5K, O.Q6K]  # matrix cores for n >= 2
 
 
 @pytest.mark.parametrize("ty", O.GGML_TYPES, ids=lambda t: O.TYPE_NAMES[t])
@@ -61,8 +61,8 @@ def test_product_matches_self_check(ctx, ty):
 @pytest.mark.parametrize("ty", MM_TYPES + [O.BF16, O.F32], ids=lambda t: O.TYPE_NAMES[t])
 def test_product_at_model_widths(ctx, ty):
     """Model-width rows (4096 weights: 128 groups), a row count that is not a multiple of a
-    workgroup's 16, and 13 input rows (matrix cores; BF16 and F32 two VALU passes of 8) and 5
-    (one VALU pass)."""
+    workgroup's 16, and 13 and 5 input rows (the matrix cores; BF16 and F32 in VALU passes of
+    8)."""
     rows, cols = 301, 4096
     data = O.random_tensor(ty, rows, cols, 5)
     for n in (13, 5):
@@ -74,10 +74,11 @@ def test_product_at_model_widths(ctx, ty):
 @pytest.mark.parametrize("ty", [O.Q4K, O.Q4_0, O.Q6K, O.F16, O.BF16], ids=lambda t: O.TYPE_NAMES[t])
 def test_product_rows_do_not_depend_on_the_batch(ctx, ty):
     """kernels.h:9-11: a row's result never depends on how many rows share the batch, and
-    reruns give the same bits: among batches of 8 or more (the matrix-core product: the
-    same row at another place of another batch) and among passes of fewer than 8. Between
-    the two a row agrees within rounding (the reference's batched product sums in another
-    order too, gpu/mod.rs:35-37)."""
+    reruns give the same bits: among batches of 2 or more (the matrix-core product: the same
+    row at another place of another batch), and one-row passes among themselves. A batch row
+    agrees with the same row passed alone within rounding, as the reference's does
+    (gpu/mod.rs:35-37: its batched product sums in another order too); BF16 (no matrix-core
+    form) gives the same bits either way."""
     rows, cols, n = 70, 1024, 19
     data = O.random_tensor(ty, rows, cols, 9)
     x = np.random.default_rng(4).standard_normal((n, cols)).astype(np.float32)
@@ -85,14 +86,18 @@ def test_product_rows_do_not_depend_on_the_batch(ctx, ty):
     np.testing.assert_array_equal(whole, product(ctx, ty, data, rows, cols, x, n))
     np.testing.assert_array_equal(product(ctx, ty, data, rows, cols, x[3:11], 8), whole[3:11])
     np.testing.assert_array_equal(product(ctx, ty, data, rows, cols, x[5:19], 14), whole[5:19])
-    small = product(ctx, ty, data, rows, cols, x[3:10], 7)
-    for i in (3, 5, 9):
-        np.testing.assert_array_equal(product(ctx, ty, data, rows, cols, x[i:i + 1], 1)[0], small[i - 3])
+    np.testing.assert_array_equal(product(ctx, ty, data, rows, cols, x[3:10], 7), whole[3:10])
+    np.testing.assert_array_equal(product(ctx, ty, data, rows, cols, x[4:6], 2), whole[4:6])
+    alone = np.stack([product(ctx, ty, data, rows, cols, x[i:i + 1], 1)[0] for i in range(3, 10)])
+    np.testing.assert_array_equal(product(ctx, ty, data, rows, cols, x[5:6], 1)[0], alone[2])
+    if ty not in MM_TYPES:
+        np.testing.assert_array_equal(alone, whole[3:10])
+        return
     # Both are f32 sums of the same terms in other orders (each within ~3e-7 of the f64
     # product, relative to the row's largest output): bound the difference by the row's scale.
     top = 1.0 + np.abs(whole[3:10].astype(np.float64)).max(axis=1, keepdims=True)
-    d = np.abs(small.astype(np.float64) - whole[3:10]) / top
-    print(f"{O.TYPE_NAMES[ty]}: a batch row against the same row in a pass of 7: {d.max():.3g} of the row's scale",
+    d = np.abs(alone.astype(np.float64) - whole[3:10]) / top
+    print(f"{O.TYPE_NAMES[ty]}: a batch row against the same row passed alone: {d.max():.3g} of the row's scale",
           flush=True)
     assert d.max() <= 2e-6
 
@@ -114,13 +119,14 @@ def test_product_k_splits_serial_and_parallel_agree(ctx, ty):
 
 def test_f16_subnormal_weights_on_the_matrix_cores(ctx):
     """F16 weights below 2^-14 (subnormal) count in the matrix-core product as they do on the
-    VALU: a batch of 8 against a pass of 7 over weights of scale 2e-5 (most subnormal)."""
+    VALU: a batch of 8 against one-row passes over weights of scale 2e-5 (most subnormal)."""
     rows, cols = 64, 1024
     w = (np.random.default_rng(12).standard_normal((rows, cols)) * 2e-5).astype(np.float16)
     assert (np.abs(w) < 2.0 ** -14).mean() > 0.9
     x = np.random.default_rng(13).standard_normal((8, cols)).astype(np.float32)
-    batch = product(ctx, O.F16, w.view(np.uint8).reshape(-1), rows, cols, x, 8)
-    small = product(ctx, O.F16, w.view(np.uint8).reshape(-1), rows, cols, x[:7], 7)
+    wb = w.view(np.uint8).reshape(-1)
+    batch = product(ctx, O.F16, wb, rows, cols, x, 8)
+    small = np.stack([product(ctx, O.F16, wb, rows, cols, x[i:i + 1], 1)[0] for i in range(7)])
     top = np.abs(small.astype(np.float64)).max(axis=1, keepdims=True)
     d = np.abs(batch[:7].astype(np.float64) - small) / top
     print(f"F16 subnormal weights: batch against VALU pass {d.max():.3g} of the row's scale", flush=True)

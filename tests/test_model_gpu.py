@@ -120,10 +120,11 @@ def test_a_split_model_computes_what_the_whole_one_does(ctx, neox):
 @pytest.mark.parametrize("neox", [False, True])
 def test_a_tree_pass_scores_every_path_as_if_fed_alone(ctx, neox):
     """model.rs:538-611 on the GPU: tree rows equal their lines bit for bit; the same tree
-    grown a level at a time scores every node the same (here also the lone-row level: a
-    tree row of any batch takes the same attention arithmetic); after Cache::keep of the
-    accepted path the next step matches the text fed whole within 1e-4 x (1 + the largest
-    score) (model.rs:595-601)."""
+    grown a level at a time scores every node the same, bit for bit where the level is a
+    batch and within 1e-4 x (1 + the largest score) for the lone-row level (whose products
+    run on the VALU, the reference's `!on_gpu || node < 4`, model.rs:593); after Cache::keep
+    of the accepted path the next step matches the text fed whole within 1e-4 x (1 + the
+    largest score) (model.rs:595-601)."""
     model = tiny_model(3, neox)
     part = Part(ctx, model, 0, 3, True)
     prefix = [5, 9, 13]
@@ -149,7 +150,10 @@ def test_a_tree_pass_scores_every_path_as_if_fed_alone(ctx, neox):
         x = part.forward(embed(part.embd, order[lo:hi]), len(prefix) + lo, parents[:hi], grown)
         seen.extend(part.g.logits(x, hi - lo))
     for node, row in [(0, 0), (1, 4), (2, 1), (3, 2), (4, 3)]:
-        np.testing.assert_array_equal(seen[node], scores[row], err_msg=f"node {node}")
+        if node < 4:
+            np.testing.assert_array_equal(seen[node], scores[row], err_msg=f"node {node}")
+        else:
+            close(seen[node], scores[row].astype(np.float64), 1e-4, f"node {node} (a lone-row level)")
     # Accept 40 -> 41 -> 43 (rows 0, 1, 3).
     kv.keep(len(prefix), [0, 1, 3])
     nxt = run([part], [kv], [50], 6)
