@@ -207,7 +207,8 @@ def test_split_and_unsplit_give_the_same_bits(ctx):
     chunk, combined): identical bits, the chunk fold being fixed. Every row of a large pass
     (enough workgroups for the wide kernel: one online softmax over each row's whole list)
     against those passes: within 1e-4, the reference's bound for a batch row against a
-    one-token pass (model.rs:641-642)."""
+    one-token pass (model.rs:641-642); reruns of the large pass give the same bits
+    (model.rs:648)."""
     nh, nkv, hd = 32, 8, 128
     pos = 3000
     big = 2100  # 8 kv heads x 66 row blocks of 32: enough workgroups to run unsplit
@@ -216,6 +217,8 @@ def test_split_and_unsplit_give_the_same_bits(ctx):
     kc, vc = rand((n, nkv * hd), 16), rand((n, nkv * hd), 17)
     a = Attn(ctx, kc, vc, bchip.F16, nh, nkv, hd)
     whole = a.run(q, big, pos, 0.0884)
+    for _ in range(3):
+        np.testing.assert_array_equal(a.run(q, big, pos, 0.0884), whole, err_msg="wide pass rerun")
     worst = 0.0
     for r0 in range(0, big, 200):
         n = min(200, big - r0)
