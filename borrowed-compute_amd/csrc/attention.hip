@@ -550,12 +550,22 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, n = lane & 15;
     const uint32_t u = blockIdx.x * 4u + w;  // this wave's unit
-    if (u >= p.nunits) return;               // no barrier below: a wave may leave alone
-    uint32_t it = 0;
-    while (it + 1 < p.nitems && u >= p.items[it + 1].unit0) it++;
-    const Item I = p.items[it];
-    const uint32_t pos0 = FUSE ? p.positions[I.row] : 0u;  // before any store: a scalar load
+    // The arguments are read before any branch on them, so that their scalar loads go out
+    // together (one round trip to memory at the start rather than one for the unit count,
+    // one for the item count and one for the item); a launch of one item needs no search.
+    const uint32_t nunits = p.nunits, nitems = p.nitems;
+    Item I = p.items[0];
     const uint32_t hd = p.hd, kvd = p.nkv * hd, G = p.G;
+    asm volatile("" ::"s"(nunits), "s"(nitems), "s"(I.row), "s"(I.len), "s"(I.unit0), "s"(I.nchunk), "s"(I.chunk),
+                 "s"(I.kvoff), "s"(hd), "s"(kvd), "s"(G), "s"(p.kc), "s"(p.vc), "s"(p.q), "s"(p.positions), "s"(p.zero),
+                 "s"(p.nh), "s"(p.sc), "s"(p.knew), "s"(p.vnew), "s"(p.inv_freq), "s"(p.rope_dim), "s"(p.neox));
+    if (u >= nunits) return;  // no barrier below: a wave may leave alone
+    uint32_t it = 0;
+    if (nitems > 1) {
+        while (it + 1 < nitems && u >= p.items[it + 1].unit0) it++;
+        I = p.items[it];
+    }
+    const uint32_t pos0 = FUSE ? p.positions[I.row] : 0u;  // before any store: a scalar load
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = rem % p.nkv;
     const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, I.len);
     // The last chunk streams up to the list's last entry and then takes that entry alone:
@@ -925,18 +935,19 @@ __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectPa
     constexpr uint32_t NDS = (HD + ROW_FOLD_DIMS - 1) / ROW_FOLD_DIMS;  // dim slices
     __shared__ float4 rO[R][D4];
     __shared__ float2 rML[R][D4];
-    const uint32_t b = blockIdx.x / NDS, ds = blockIdx.x % NDS, per_item = p.nkv * p.G;
+    // The arguments are read before any branch on them (their scalar loads go out together);
+    // a launch of one item needs no indexed read of the item.
+    const uint32_t nitems = p.nitems, nkv = p.nkv, G = p.G;
+    Item I = p.items[0];
+    asm volatile("" ::"s"(nitems), "s"(nkv), "s"(G), "s"(I.row), "s"(I.unit0), "s"(I.nchunk), "s"(p.hd), "s"(p.nh),
+                 "s"(p.fuse), "s"(p.out), "s"(p.part_o), "s"(p.part_ml), "s"(p.qw), "s"(p.qrot));
+    const uint32_t b = blockIdx.x / NDS, ds = blockIdx.x % NDS, per_item = nkv * G;
     const uint32_t item = b / per_item;
-    const Item I = p.items[item];
+    if (nitems > 1) I = p.items[item];
     const uint32_t nch = I.nchunk;
     if (nch <= 1) return;  // written by the decode kernel
     const uint32_t kvh = (b % per_item) / p.G, s = (b % per_item) % p.G;
     const uint32_t tid = threadIdx.x, r = tid / D4, d = ds * ROW_FOLD_DIMS + 4 * (tid % D4);
-    if (p.fuse && tid < ROW_FOLD_DIMS && ds * ROW_FOLD_DIMS + tid < p.hd) {
-        // A fused step: every unit has read q; leave head kvh * G + s rotated.
-        const size_t h = (size_t)kvh * p.G + s, e = ds * ROW_FOLD_DIMS + tid;
-        p.qw[((size_t)I.row * p.nh + h) * p.hd + e] = p.qrot[((size_t)item * p.nh + h) * p.hd + e];
-    }
     const size_t cu0 = (size_t)I.unit0 + (size_t)kvh * nch;
     float2 ml[NPT];
     float4 ov[NPT];
@@ -946,6 +957,12 @@ __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectPa
         const size_t at = (cu0 + (c < nch ? c : 0u)) * 16 + s;
         ml[q] = *(const float2*)(p.part_ml + at * 2);
         ov[q] = *(const float4*)(p.part_o + at * HD + d);
+    }
+    // After the state loads are out (a store before them would hold them behind its load).
+    if (p.fuse && tid < ROW_FOLD_DIMS && ds * ROW_FOLD_DIMS + tid < p.hd) {
+        // A fused step: every unit has read q; leave head kvh * G + s rotated.
+        const size_t h = (size_t)kvh * p.G + s, e = ds * ROW_FOLD_DIMS + tid;
+        p.qw[((size_t)I.row * p.nh + h) * p.hd + e] = p.qrot[((size_t)item * p.nh + h) * p.hd + e];
     }
     float M = -INFINITY, L = 0.0f;
     float4 O = float4{0.0f, 0.0f, 0.0f, 0.0f};
