@@ -1152,30 +1152,36 @@ constexpr int CMB_THREADS = 64;
 
 template <int HD, int RUN>
 __global__ __launch_bounds__(CMB_THREADS) void attn_combine(const CombineParams p) {
-    const uint32_t nd4 = p.hd / 4;
+    // The arguments are read before any branch on them, so that their scalar loads go out
+    // together (one round trip to memory rather than one per branch).
+    const uint32_t hd = p.hd, slots_out = p.slots_out, ngroups = p.ngroups, shared = p.shared, nrb = p.nrb,
+                   rb = p.rb, G = p.G, rows = p.rows, nch_s = p.nchunk, nkv = p.nkv;
+    asm volatile("" ::"s"(hd), "s"(slots_out), "s"(ngroups), "s"(shared), "s"(nrb), "s"(rb), "s"(G), "s"(rows),
+                 "s"(nch_s), "s"(nkv), "s"(p.nh), "s"(p.slots), "s"(p.out), "s"(p.part_o), "s"(p.part_ml));
+    const uint32_t nd4 = hd / 4;
     const uint32_t t = blockIdx.x * CMB_THREADS + threadIdx.x;
     const uint32_t d4 = t % nd4, rest = t / nd4;
-    const uint32_t slot = rest % p.slots_out, grp = rest / p.slots_out;
-    if (grp >= p.ngroups) return;
+    const uint32_t slot = rest % slots_out, grp = rest / slots_out;
+    if (grp >= ngroups) return;
     uint32_t unit0, nchunk, r, h, step;  // chunk c's state is unit unit0 + c * step
-    if (p.shared) {
-        const uint32_t kvh = grp / p.nrb, rbi = grp % p.nrb;
-        const uint32_t gh = slot / p.rb, rl = slot % p.rb;
-        r = rbi * p.rb + rl;
-        if (gh >= p.G || r >= p.rows) return;
-        h = kvh * p.G + gh;
-        unit0 = grp * p.nchunk;
-        nchunk = p.nchunk;
+    if (shared) {
+        const uint32_t kvh = grp / nrb, rbi = grp % nrb;
+        const uint32_t gh = slot / rb, rl = slot % rb;
+        r = rbi * rb + rl;
+        if (gh >= G || r >= rows) return;
+        h = kvh * G + gh;
+        unit0 = grp * nch_s;
+        nchunk = nch_s;
         step = 1;
     } else {  // decode kernel states, in (item, chunk, KV head) order
-        const uint32_t item = grp / p.nkv, kvh = grp % p.nkv;
+        const uint32_t item = grp / nkv, kvh = grp % nkv;
         const Item& I = p.items[item];
-        if (slot / p.G >= I.nrows || I.nchunk == 1) return;  // one chunk: written directly
-        r = I.row + slot / p.G;
-        h = kvh * p.G + slot % p.G;
+        if (slot / G >= I.nrows || I.nchunk == 1) return;  // one chunk: written directly
+        r = I.row + slot / G;
+        h = kvh * G + slot % G;
         unit0 = I.unit0 + kvh;
         nchunk = I.nchunk;
-        step = p.nkv;
+        step = nkv;
     }
     const size_t stride = p.slots;  // partial slots per unit
     float M = -INFINITY, L = 0.0f;
