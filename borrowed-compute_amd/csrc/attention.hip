@@ -933,8 +933,8 @@ __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectPa
     constexpr uint32_t R = ROW_FOLD_THREADS / D4;           // subsets
     constexpr uint32_t NPT = (ROW_MAX_CHUNKS + R - 1) / R;  // chunks per subset at most
     constexpr uint32_t NDS = (HD + ROW_FOLD_DIMS - 1) / ROW_FOLD_DIMS;  // dim slices
-    __shared__ float4 rO[R][D4];
-    __shared__ float2 rML[R][D4];
+    __shared__ float4 rO[ROW_FOLD_THREADS / 64][D4];
+    __shared__ float2 rML[ROW_FOLD_THREADS / 64][D4];
     // The arguments are read before any branch on them (their scalar loads go out together);
     // a launch of one item needs no indexed read of the item.
     const uint32_t nitems = p.nitems, nkv = p.nkv, G = p.G;
@@ -976,22 +976,50 @@ __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectPa
             M = mn;
         }
     }
-    rO[r][tid % D4] = O;
-    rML[r][tid % D4] = float2{M, L};
-#pragma unroll
-    for (uint32_t step = 1; step < R; step *= 2) {
-        __syncthreads();
-        if (r % (2 * step) == 0) {
-            const float2 o2 = rML[r + step][tid % D4];
-            const float4 oo = rO[r + step][tid % D4];
-            float a, bb, mn;
-            merge_coef(M, o2.x, a, bb, mn);
-            L = L * a + o2.y * bb;
-            O = float4{O.x * a + oo.x * bb, O.y * a + oo.y * bb, O.z * a + oo.z * bb, O.w * a + oo.w * bb};
-            M = mn;
-            rO[r][tid % D4] = O;
-            rML[r][tid % D4] = float2{M, L};
-        }
+    // The binary tree over the subsets (r with r + 1, then r with r + 2, ...): its levels
+    // within a wave (eight subsets of D4 lanes: partners 8, 16 and 32 lanes up) by cross-lane
+    // moves, without a barrier; the two across the workgroup's waves through LDS. A lane
+    // whose subset is not a left operand at a level computes a value no one reads.
+    auto merge = [&](float m2, float l2, float4 o2) {
+        float a, bb, mn;
+        merge_coef(M, m2, a, bb, mn);
+        L = L * a + l2 * bb;
+        O = float4{O.x * a + o2.x * bb, O.y * a + o2.y * bb, O.z * a + o2.z * bb, O.w * a + o2.w * bb};
+        M = mn;
+    };
+    static_assert(D4 == 8 && ROW_FOLD_THREADS == 256, "eight subsets a wave, four waves");
+    {
+        // partner 8 lanes up: DPP rotation by 8 within each row of 16 lanes
+        auto up8 = [](float x) {
+            return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+        };
+        merge(up8(M), up8(L), float4{up8(O.x), up8(O.y), up8(O.z), up8(O.w)});
+        // partners 16 and 32 lanes up: the upper value of a permlane swap's pair
+        auto up16 = [](float x) {
+            return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+        };
+        merge(up16(M), up16(L), float4{up16(O.x), up16(O.y), up16(O.z), up16(O.w)});
+        auto up32 = [](float x) {
+            return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+        };
+        merge(up32(M), up32(L), float4{up32(O.x), up32(O.y), up32(O.z), up32(O.w)});
+    }
+    const uint32_t wv = tid / 64, q = tid % 64;  // wave; subset 8 wv holds the wave's state in lanes q < D4
+    if (q < D4) {
+        rO[wv][q] = O;
+        rML[wv][q] = float2{M, L};
+    }
+    __syncthreads();
+    if (q < D4 && wv % 2 == 0) {
+        const float2 o2 = rML[wv + 1][q];
+        merge(o2.x, o2.y, rO[wv + 1][q]);
+        rO[wv][q] = O;
+        rML[wv][q] = float2{M, L};
+    }
+    __syncthreads();
+    if (q < D4 && wv == 0) {
+        const float2 o2 = rML[2][q];
+        merge(o2.x, o2.y, rO[2][q]);
     }
     if (r == 0 && d < p.hd)
         *(float4*)(p.out + ((size_t)I.row * p.nh + kvh * p.G + s) * p.hd + d) = float4{O.x / L, O.y / L, O.z / L, O.w / L};
