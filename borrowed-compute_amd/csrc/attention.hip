@@ -922,8 +922,8 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
 // head, slot, ROW_FOLD_DIMS dims), so the loads spread over many CUs. R thread subsets of
 // ROW_FOLD_DIMS / 4 threads (four dims each): subset r folds chunks r, r + R, r + 2R, ...
 // in that order from a cleared state (all its loads issued before the first use), then the
-// R subset states merge as a binary tree in LDS (r with r + 1, then r with r + 2, ...) and
-// the root is normalised. The order is fixed by the chunk count and the shape alone.
+// R subset states merge as a binary tree (r with r + 1, then r with r + 2, ...) and the root
+// is normalised. The order is fixed by the chunk count and the shape alone.
 constexpr int ROW_FOLD_THREADS = 256;
 constexpr int ROW_FOLD_DIMS = 32;
 
