@@ -275,9 +275,19 @@ struct Raw<float> {
 
 // 8 elements of a Q row times sc (the attention scale times log2(e), so that scores come
 // out of the MFMA in exp2 units), rounded to f16: the B operand of the score MFMAs.
+// The product is rounded to f32 and then to f16 in every kernel: the empty asm keeps the
+// compiler from folding multiply and conversion into one mixed-precision FMA
+// (v_fma_mixlo_f16), which rounds the exact product to f16 once and so differs from the
+// two roundings in rare elements (it did so in some kernels and not others, by register
+// allocation, which broke bit-identity between kernels that share this arithmetic).
+__device__ __forceinline__ f16 scaled_f16(float x, float sc) {
+    float y = x * sc;
+    asm("" : "+v"(y));
+    return (f16)y;
+}
 __device__ __forceinline__ half8 q_scaled(float4 a, float4 b, float sc) {
-    return half8{(f16)(a.x * sc), (f16)(a.y * sc), (f16)(a.z * sc), (f16)(a.w * sc),
-                 (f16)(b.x * sc), (f16)(b.y * sc), (f16)(b.z * sc), (f16)(b.w * sc)};
+    return half8{scaled_f16(a.x, sc), scaled_f16(a.y, sc), scaled_f16(a.z, sc), scaled_f16(a.w, sc),
+                 scaled_f16(b.x, sc), scaled_f16(b.y, sc), scaled_f16(b.z, sc), scaled_f16(b.w, sc)};
 }
 
 __device__ __forceinline__ half8 q_operand(const float* __restrict__ qrow, uint32_t hd0, uint32_t hd, bool ok, float sc) {
@@ -337,7 +347,12 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 && HD <= 128 ? 4 : 2) void at
     // channels finishing last. The state is stored at the unit's canonical index.
     const uint32_t u = blockIdx.x;
     uint32_t it = 0;
-    while (it + 1 < p.nitems && u >= p.items[it + 1].unit0) it++;
+    if (p.nitems > 1) {
+        // The last item whose first unit is at or below u (items hold their units in order),
+        // every item's first unit read by one lane at once (MAX_ITEMS is the wave size).
+        const uint32_t u0 = p.items[(uint32_t)lane < p.nitems ? lane : 0].unit0;
+        it = (uint32_t)__popcll(__ballot((uint32_t)lane < p.nitems && u0 <= u)) - 1u;
+    }
     const Item I = p.items[it];
     const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = (rem % p.nkv + c) % p.nkv;
     const size_t cu = (size_t)I.unit0 + (size_t)c * p.nkv + kvh;
@@ -562,7 +577,11 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     if (u >= nunits) return;  // no barrier below: a wave may leave alone
     uint32_t it = 0;
     if (nitems > 1) {
-        while (it + 1 < nitems && u >= p.items[it + 1].unit0) it++;
+        // The unit's item: the last whose first unit is at or below u (items hold their
+        // units in order), every item's first unit read by one lane at once (MAX_ITEMS is
+        // the wave size).
+        const uint32_t u0 = p.items[(uint32_t)lane < nitems ? lane : 0].unit0;
+        it = (uint32_t)__popcll(__ballot((uint32_t)lane < nitems && u0 <= u)) - 1u;
         I = p.items[it];
     }
     const uint32_t pos0 = FUSE ? p.positions[I.row] : 0u;  // before any store: a scalar load

@@ -24,7 +24,7 @@ constexpr uint32_t CHUNK_MULTI = 192;
 // Largest head dimension (the reference's MAX_HEAD, kernels.h:31).
 constexpr uint32_t MAX_HD = 256;
 // Rows a tree pass may hold (model.rs:408), and items one direct launch takes.
-constexpr uint32_t MAX_ITEMS = 64;
+constexpr uint32_t MAX_ITEMS = 64;  // at most one a lane: a wave finds a unit's item by one ballot
 
 constexpr float LOG2E = 1.4426950408889634f;
 
