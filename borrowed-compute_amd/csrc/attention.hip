@@ -1383,6 +1383,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     __shared__ __attribute__((aligned(16))) f16 ring0[SZ];
     __shared__ __attribute__((aligned(16))) f16 ring1[SZ];
     __shared__ __attribute__((aligned(16))) f16 ring2[SZ];
+    // Each wave's Q tile as loaded: 2 * NKC rows of 64 lanes x 4 floats.
+    __shared__ __attribute__((aligned(16))) float qlds[W][2 * NKC * 256];
     auto ring = [&](auto S) -> f16* {
         if constexpr (decltype(S)::value == 0) return ring0;
         else if constexpr (decltype(S)::value == 1) return ring1;
@@ -1406,7 +1408,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     // loaded here and converted after the first K/V loads are issued, so that the two
     // latencies overlap.
     half8 qb[NKC];
-    float4 qraw[NKC][2];
     uint32_t len, orow, ohead;
     bool valid;
     {
@@ -1417,11 +1418,16 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         orow = r;
         ohead = kvh * p.G + gh;
         const float* qrow = valid ? p.q + ((size_t)r * p.nh + ohead) * HD : (const float*)p.zero;
+        // Q goes to the wave's own LDS rows by direct-to-LDS loads, each lane's 16 bytes to
+        // its own place, like the blocks after it: the compiler counts a wait for them per
+        // LDS object, so the conversion below waits for Q alone, not for the blocks issued
+        // after it (loads into registers would be counted as the last ones issued).
+        typedef __attribute__((address_space(3))) void lds_q_t;
 #pragma unroll
         for (int c = 0; c < NKC; c++) {
             const float* src = valid ? qrow + 32 * c + 8 * g : qrow;
-            qraw[c][0] = *(const float4*)src;
-            qraw[c][1] = *(const float4*)(src + 4);
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_q_t*)&qlds[w][(2 * c) * 256], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(src + 4), (lds_q_t*)&qlds[w][(2 * c + 1) * 256], 16, 0, 0);
         }
     }
     uint32_t kb0, kb1;
@@ -1453,6 +1459,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         }
     }
     typedef __attribute__((address_space(3))) void lds_t;
+    // A block within the list issues LPB loads per wave, rows past the list from the zero
+    // page; a block past the list issues none.
     auto load_block = [&](uint32_t key0, auto S) {
         if (key0 >= kb1) return;  // nothing past the list
         f16* kl = ring(S);
@@ -1501,13 +1509,40 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     state_clear(R);
     state_clear(cs);
     // Prologue: blocks 0 .. STAGES-2 in flight. (A workgroup of a split launch may see
-    // nothing of its chunk: then it only stores its empty states.)
-    if (kb0 < kb1) {
-        load_block(kb0, ic<0>{});
-        load_block(kb0 + BLK, ic<1>{});
-    }
+    // nothing of its chunk: then it only stores its empty states.) Q waits only for its own
+    // loads, which went out before the blocks' (a wave's loads complete in issue order): the
+    // blocks stay in flight through the conversion. The waits count the blocks' loads
+    // exactly, and the LDS reads of Q are written out, so that the compiler does not add
+    // its own wait for every load in flight before them (it does not count direct-to-LDS
+    // loads as younger than Q's).
+    load_block(kb0, ic<0>{});
+    load_block(kb0 + BLK, ic<1>{});
+    if (kb0 + BLK < kb1)
+        wait_vm<2 * LPB>();
+    else if (kb0 < kb1)
+        wait_vm<LPB>();
+    else
+        wait_vm<0>();
+    {
+        const uint32_t qa = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&qlds[w][4 * lane];
+        f32x4 qv[2 * NKC];
+        asm volatile(
+            "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:1024\n\t"
+            "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %8 offset:3072\n\t"
+            "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %8 offset:5120\n\t"
+            "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %8 offset:7168\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(qv[0]), "=&v"(qv[1]), "=&v"(qv[2]), "=&v"(qv[3]), "=&v"(qv[4]), "=&v"(qv[5]), "=&v"(qv[6]),
+              "=&v"(qv[7])
+            : "v"(qa)
+            : "memory");
+        static_assert(NKC == 4, "eight 1 KB rows of Q a wave");
 #pragma unroll
-    for (int c = 0; c < NKC; c++) qb[c] = q_scaled(qraw[c][0], qraw[c][1], p.sc);
+        for (int c = 0; c < NKC; c++) {
+            const f32x4 a = qv[2 * c], b = qv[2 * c + 1];
+            qb[c] = q_scaled(float4{a[0], a[1], a[2], a[3]}, float4{b[0], b[1], b[2], b[3]}, p.sc);
+        }
+    }
 
     // One block in stage S: scores, mask, softmax, PV.
     auto iter = [&](uint32_t key0, auto S) -> bool {
