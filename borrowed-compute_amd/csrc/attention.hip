@@ -143,6 +143,33 @@ __device__ __forceinline__ half4 lds_tr4(const f16* p) {
     return __builtin_bit_cast(half4, v);
 }
 
+// Eight transposing reads (rows a_j and a_j + 16 rows of 256 bytes) and the wait for them,
+// as one statement: the results exist only once it is done, so nothing can read them early,
+// and the compiler adds no wait of its own (it would wait for every direct-to-LDS load in
+// flight, not knowing these reads miss the stages still filling). The caller must know
+// the rows' data has landed in LDS.
+__device__ __forceinline__ void lds_tr4x4(half4 (&lo)[4], half4 (&hi)[4], uint32_t a0, uint32_t a1, uint32_t a2,
+                                          uint32_t a3) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    s16x4 l0, l1, l2, l3, h0, h1, h2, h3;
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %4, %8 offset:4096\n\t"
+        "ds_read_b64_tr_b16 %1, %9\n\tds_read_b64_tr_b16 %5, %9 offset:4096\n\t"
+        "ds_read_b64_tr_b16 %2, %10\n\tds_read_b64_tr_b16 %6, %10 offset:4096\n\t"
+        "ds_read_b64_tr_b16 %3, %11\n\tds_read_b64_tr_b16 %7, %11 offset:4096\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(l0), "=&v"(l1), "=&v"(l2), "=&v"(l3), "=&v"(h0), "=&v"(h1), "=&v"(h2), "=&v"(h3)
+        : "v"(a0), "v"(a1), "v"(a2), "v"(a3));
+    lo[0] = __builtin_bit_cast(half4, l0);
+    lo[1] = __builtin_bit_cast(half4, l1);
+    lo[2] = __builtin_bit_cast(half4, l2);
+    lo[3] = __builtin_bit_cast(half4, l3);
+    hi[0] = __builtin_bit_cast(half4, h0);
+    hi[1] = __builtin_bit_cast(half4, h1);
+    hi[2] = __builtin_bit_cast(half4, h2);
+    hi[3] = __builtin_bit_cast(half4, h3);
+}
+
 template <int VS>
 __device__ __forceinline__ half8 v_operand(const f16* __restrict__ vl, int dt, int kc, int g, int j) {
     const f16* src = vl + (32 * kc + 4 * g + (j >> 2)) * VS + 16 * dt + 4 * (j & 3);
@@ -1495,6 +1522,11 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     for (int c = 0; c < NKC; c++) kbase[c] = n * HD + 8 * ((4 * c + g) ^ n);
 #pragma unroll
     for (int kc = 0; kc < 2; kc++) vbase[kc] = n * BLK + 8 * ((4 * kc + g) ^ (n % 8));
+    // The transposing V reads' lane terms: row 4g + n/4 of a 32-row half (rows r and r + 16
+    // share the swizzle 2 (r % 8)), its half-chunk (n % 4) / 2 and dims half n % 2 (in f16),
+    // and the 16-dim chunk swizzle.
+    const uint32_t vrow = (4 * g + (n >> 2)) * HD + 8 * ((n & 3) >> 1) + 4 * (n & 1);
+    const uint32_t vsw = (4 * g + (n >> 2)) % 8;
     // Barrier without the fence __syncthreads carries: that fence would wait for every
     // direct-to-LDS load in flight, the later blocks' included. The waits before it are
     // explicit; LDS reads of a wave finish before its MFMAs consume them, so every read of a
@@ -1583,23 +1615,48 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         // PV of the block.
         const f16* vls = ring(S) + BLK * HD;
 #pragma unroll
-        for (int kc = 0; kc < 2; kc++)
+        for (int kc = 0; kc < 2; kc++) {
+            if constexpr (VT) {
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++) {
-                half8 a;
-                if constexpr (VT) {
-                    a = *(const half8*)&vls[vbase[kc] + dt * 16 * BLK];
-                } else {
+                for (int dt = 0; dt < NDT; dt++)
+                    cs.o[dt] = mfma16(*(const half8*)&vls[vbase[kc] + dt * 16 * BLK], pb[kc], cs.o[dt]);
+            } else if constexpr (W == 4) {
+                // Transposing reads (source lane j of its 16-lane group names row kbase + j/4,
+                // dims 16dt + 4(j%4): chunk 2dt + (j%4)/2, half (j%4)%2), written out with one
+                // wait per four dims tiles: the compiler's intrinsic would carry a wait for
+                // every load in flight (it cannot tell these reads miss the stages still
+                // filling), holding the block's PV until the block two ahead lands. This
+                // stage's own loads landed before the block's barrier. Row r and r + 16 share
+                // the swizzle, so a read's address is the lane's row base plus 16 dims' chunk
+                // (dt ^ s) * 32 bytes, and the second half of the rows an immediate offset.
+                static_assert(16 * HD * 2 == 4096, "lds_tr4x4's second rows sit 16 rows of hd 128 on");
+                uint32_t rowb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const f16*)&vls[vrow + kc * 32 * HD];
+                asm("" : "+v"(rowb));  // per block: not hoisted into registers for every stage
+#pragma unroll
+                for (int d0 = 0; d0 < NDT; d0 += 4) {
+                    half4 lo[4], hi[4];
+                    lds_tr4x4(lo, hi, rowb + 32u * ((uint32_t)(d0 + 0) ^ vsw), rowb + 32u * ((uint32_t)(d0 + 1) ^ vsw),
+                              rowb + 32u * ((uint32_t)(d0 + 2) ^ vsw), rowb + 32u * ((uint32_t)(d0 + 3) ^ vsw));
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const half8 a = half8{lo[j][0], lo[j][1], lo[j][2], lo[j][3], hi[j][0], hi[j][1], hi[j][2], hi[j][3]};
+                        cs.o[d0 + j] = mfma16(a, pb[kc], cs.o[d0 + j]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) {
                     // transposing read: source lane j of its 16-lane group names row
                     // kbase + j/4, dims 16dt + 4(j%4): chunk 2dt + (j%4)/2, half (j%4)%2
                     const uint32_t r = 32 * kc + 4 * g + (n >> 2), ch = 2 * dt + ((n & 3) >> 1), h = n & 1;
                     const half4 lo = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
                     const uint32_t r2 = r + 16;
                     const half4 hi = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
-                    a = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    const half8 a = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    cs.o[dt] = mfma16(a, pb[kc], cs.o[dt]);
                 }
-                cs.o[dt] = mfma16(a, pb[kc], cs.o[dt]);
             }
+        }
         return key1 < kb1;
     };
     // Chunk by chunk: three blocks, then (when the list goes on) the chunk's fold into R and
