@@ -88,19 +88,41 @@ int enter(bchip_ctx* c) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// For memory this library allocated, that [p, p + bytes) lies inside one allocation.
-// Memory from elsewhere cannot be checked and is trusted.
-int check_span(const bchip_ctx* c, const void* p, uint64_t bytes, const char* what) {
-    if (c->allocs.empty() || bytes == 0) return BCHIP_OK;
+// Byte counts from element counts, saturated: a count that overflows 64 bits becomes
+// UINT64_MAX, which no span check accepts.
+uint64_t sat_add(uint64_t a, uint64_t b) {
+    uint64_t r;
+    return __builtin_add_overflow(a, b, &r) ? UINT64_MAX : r;
+}
+uint64_t sat_mul(uint64_t a, uint64_t b) {
+    uint64_t r;
+    return __builtin_mul_overflow(a, b, &r) ? UINT64_MAX : r;
+}
+
+// [p + off, p + off + bytes) must not wrap the address space (whoever allocated p), and,
+// when p lies in memory this library allocated, must lie inside that allocation. Memory
+// from elsewhere cannot be checked further and is trusted.
+int check_at(const bchip_ctx* c, const void* p, uint64_t off, uint64_t bytes, const char* what) {
+    if (bytes == 0) return BCHIP_OK;
     const uintptr_t a = (uintptr_t)p;
+    if (off == UINT64_MAX || bytes == UINT64_MAX || off > UINTPTR_MAX - a || bytes > UINTPTR_MAX - a - off)
+        return fail(BCHIP_E_ARG, "%s: a span of %llu bytes at offset %llu passes the end of the address space", what,
+                    (unsigned long long)bytes, (unsigned long long)off);
+    if (c->allocs.empty()) return BCHIP_OK;
     auto it = c->allocs.upper_bound(a);
     if (it == c->allocs.begin()) return BCHIP_OK;
     --it;
     if (a >= it->first + it->second) return BCHIP_OK;  // not ours
-    if (a + bytes > it->first + it->second)
+    const uint64_t left = it->first + it->second - a;  // bytes from p to the allocation's end
+    if (off > left || bytes > left - off)
         return fail(BCHIP_E_ARG, "%s: %llu bytes from offset %llu pass the end of its %llu-byte buffer", what,
-                    (unsigned long long)bytes, (unsigned long long)(a - it->first), (unsigned long long)it->second);
+                    (unsigned long long)bytes, (unsigned long long)(a - it->first + off),
+                    (unsigned long long)it->second);
     return BCHIP_OK;
+}
+
+int check_span(const bchip_ctx* c, const void* p, uint64_t bytes, const char* what) {
+    return check_at(c, p, 0, bytes, what);
 }
 
 uint32_t esize(uint32_t type) { return type == BCHIP_F16 ? 2u : 4u; }
@@ -334,7 +356,7 @@ int bchip_upload(bchip_ctx* c, void* dev, size_t off, const void* host, size_t b
     CHECK(enter(c));
     if (bytes == 0) return BCHIP_OK;
     if (!dev || !host) return fail(BCHIP_E_ARG, "null pointer");
-    CHECK(check_span(c, (char*)dev + off, bytes, "upload"));
+    CHECK(check_at(c, dev, off, bytes, "upload"));
     HIP_TRY(hipMemcpyAsync((char*)dev + off, host, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return BCHIP_OK;
@@ -344,7 +366,7 @@ int bchip_download(bchip_ctx* c, const void* dev, size_t off, void* host, size_t
     CHECK(enter(c));
     if (bytes == 0) return BCHIP_OK;
     if (!dev || !host) return fail(BCHIP_E_ARG, "null pointer");
-    CHECK(check_span(c, (const char*)dev + off, bytes, "download"));
+    CHECK(check_at(c, dev, off, bytes, "download"));
     HIP_TRY(hipMemcpyAsync(host, (const char*)dev + off, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return BCHIP_OK;
@@ -369,7 +391,7 @@ int bchip_rope(bchip_ctx* c, float* x, const float* inv_freq, const uint32_t* po
     if (rows == 0 || heads == 0) return BCHIP_OK;
     if (!x || !inv_freq || !positions) return fail(BCHIP_E_ARG, "null pointer");
     if (rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
-    CHECK(check_span(c, x, (uint64_t)rows * heads * hd * 4, "x"));
+    CHECK(check_span(c, x, sat_mul(sat_mul(rows, heads), (uint64_t)hd * 4), "x"));
     CHECK(check_span(c, positions, (uint64_t)rows * 4, "positions"));
     CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
     HIP_TRY(rope_launch(x, inv_freq, positions, rows, heads, hd, rope_dim, neox, c->stream), "rope");
@@ -388,9 +410,9 @@ int bchip_matmul(bchip_ctx* c, const void* w, uint32_t type, const float* x, flo
     const uint64_t row_bytes = (uint64_t)cols / bw * bb;
     if (row_bytes > UINT32_MAX) return fail(BCHIP_E_ARG, "cols %u: a row of more than 4 GiB", cols);
     if (n > MATMUL_MAX_N) return fail(BCHIP_E_ARG, "%u input rows (at most %u a call)", n, MATMUL_MAX_N);
-    CHECK(check_span(c, w, row_bytes * rows, "weights"));
-    CHECK(check_span(c, x, (uint64_t)n * cols * 4, "x"));
-    CHECK(check_span(c, out, (uint64_t)n * rows * 4, "out"));
+    CHECK(check_span(c, w, sat_mul(row_bytes, rows), "weights"));
+    CHECK(check_span(c, x, sat_mul(n, (uint64_t)cols * 4), "x"));
+    CHECK(check_span(c, out, sat_mul(n, (uint64_t)rows * 4), "out"));
     void* scratch = nullptr;
     if (const size_t sb = matmul_scratch_bytes(type, rows, cols, n)) {
         HIP_TRY(c->ws.reserve_vt(sb), "matmul scratch");
@@ -406,9 +428,9 @@ int bchip_rms_norm(bchip_ctx* c, const float* x, const float* w, float* out, uin
     if (rows == 0) return BCHIP_OK;
     if (!x || !w || !out) return fail(BCHIP_E_ARG, "null pointer");
     if (cols == 0) return fail(BCHIP_E_ARG, "cols 0");
-    CHECK(check_span(c, x, (uint64_t)rows * cols * 4, "x"));
+    CHECK(check_span(c, x, sat_mul(rows, (uint64_t)cols * 4), "x"));
     CHECK(check_span(c, w, (uint64_t)cols * 4, "w"));
-    CHECK(check_span(c, out, (uint64_t)rows * cols * 4, "out"));
+    CHECK(check_span(c, out, sat_mul(rows, (uint64_t)cols * 4), "out"));
     const bool vec = cols % 4 == 0 && ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) % 16 == 0;
     HIP_TRY(rms_norm_launch(x, w, out, rows, cols, eps, vec, c->stream), "rms_norm");
     return BCHIP_OK;
@@ -419,8 +441,8 @@ static int elementwise(bchip_ctx* c, int op, float* x, const float* y, uint64_t 
     CHECK(enter(c));
     if (n == 0) return BCHIP_OK;
     if (!x || !y) return fail(BCHIP_E_ARG, "null pointer");
-    CHECK(check_span(c, x, n * 4, what));
-    CHECK(check_span(c, y, y_len * 4, what));
+    CHECK(check_span(c, x, sat_mul(n, 4), what));
+    CHECK(check_span(c, y, sat_mul(y_len, 4), what));
     HIP_TRY(elementwise_launch(op, x, y, n, dim, c->stream), what);
     return BCHIP_OK;
 }
@@ -444,8 +466,8 @@ int bchip_copy(bchip_ctx* c, const void* src, uint32_t st, void* dst, uint32_t d
     if (n == 0) return BCHIP_OK;
     if (!src || !dst) return fail(BCHIP_E_ARG, "null pointer");
     if (st > 1 || dt > 1) return fail(BCHIP_E_ARG, "element types %u, %u", st, dt);
-    CHECK(check_span(c, src, n * esize(st), "copy source"));
-    CHECK(check_span(c, (const char*)dst + off * esize(dt), n * esize(dt), "copy destination"));
+    CHECK(check_span(c, src, sat_mul(n, esize(st)), "copy source"));
+    CHECK(check_at(c, dst, sat_mul(off, esize(dt)), sat_mul(n, esize(dt)), "copy destination"));
     HIP_TRY(copy_launch(src, st, dst, dt, off, n, c->stream), "copy");
     return BCHIP_OK;
 }
@@ -457,7 +479,7 @@ int bchip_move(bchip_ctx* c, void* buf, uint32_t type, uint64_t from, uint64_t t
     if (type > 1) return fail(BCHIP_E_ARG, "element type %u", type);
     if (to > from) return fail(BCHIP_E_ARG, "move to %llu after from %llu", (unsigned long long)to,
                                 (unsigned long long)from);
-    CHECK(check_span(c, buf, (from + n) * esize(type), "move"));
+    CHECK(check_span(c, buf, sat_mul(sat_add(from, n), esize(type)), "move"));
     HIP_TRY(move_launch(buf, type, from, to, n, c->stream), "move");
     return BCHIP_OK;
 }
@@ -470,7 +492,7 @@ int bchip_cache_grow(bchip_ctx* c, const void* const* src, void* const* dst, uin
     if (type > 1) return fail(BCHIP_E_ARG, "element type %u", type);
     if (keep > total) return fail(BCHIP_E_ARG, "keep %llu past total %llu", (unsigned long long)keep,
                                   (unsigned long long)total);
-    const uint64_t kb = keep * esize(type), tb = total * esize(type);
+    const uint64_t kb = sat_mul(keep, esize(type)), tb = sat_mul(total, esize(type));
     for (uint32_t b = 0; b < nbufs; b++) {
         const uint8_t* s = keep > 0 ? (const uint8_t*)src[b] : nullptr;
         const uint8_t* d = (const uint8_t*)dst[b];
@@ -496,7 +518,7 @@ int bchip_keep(bchip_ctx* c, void* const* bufs, uint32_t nbufs, uint32_t type, u
     if (nrows > 64) return fail(BCHIP_E_ARG, "%u rows (at most 64)", nrows);
     for (uint32_t i = 0; i + 1 < nrows; i++)
         if (rows[i] >= rows[i + 1]) return fail(BCHIP_E_ARG, "rows are not an ascending path");
-    const uint64_t end = (base + rows[nrows - 1] + 1) * width * esize(type);
+    const uint64_t end = sat_mul(sat_mul(sat_add(base, (uint64_t)rows[nrows - 1] + 1), width), esize(type));
     for (uint32_t b = 0; b < nbufs; b++) {
         if (!bufs[b]) return fail(BCHIP_E_ARG, "null buffer %u", b);
         CHECK(check_span(c, bufs[b], end, "keep"));
@@ -515,11 +537,12 @@ int bchip_rope_append(bchip_ctx* c, float* q, const float* k, const float* v, vo
     if (hd % 2 || rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
     if (nh == 0 || nkv == 0) return fail(BCHIP_E_ARG, "no heads");
     const uint64_t kvd = (uint64_t)nkv * hd;
-    CHECK(check_span(c, q, (uint64_t)rows * nh * hd * 4, "q"));
-    CHECK(check_span(c, k, rows * kvd * 4, "k"));
-    CHECK(check_span(c, v, rows * kvd * 4, "v"));
-    CHECK(check_span(c, kc, (slot0 + rows) * kvd * esize(kv_type), "kc"));
-    CHECK(check_span(c, vc, (slot0 + rows) * kvd * esize(kv_type), "vc"));
+    CHECK(check_span(c, q, sat_mul(sat_mul(rows, nh), (uint64_t)hd * 4), "q"));
+    CHECK(check_span(c, k, sat_mul(rows, kvd * 4), "k"));
+    CHECK(check_span(c, v, sat_mul(rows, kvd * 4), "v"));
+    const uint64_t cache_bytes = sat_mul(sat_mul(sat_add(slot0, rows), kvd), esize(kv_type));
+    CHECK(check_span(c, kc, cache_bytes, "kc"));
+    CHECK(check_span(c, vc, cache_bytes, "vc"));
     CHECK(check_span(c, positions, (uint64_t)rows * 4, "positions"));
     CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
     HIP_TRY(rope_append_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, rows, nh, nkv, hd, rope_dim, neox,
@@ -546,10 +569,10 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
         CHECK(check_span(c, masks, (uint64_t)rows * 8, "masks"));
     }
     const uint64_t kvd = (uint64_t)nkv * hd, slots = (uint64_t)pos + rows;
-    CHECK(check_span(c, q, (uint64_t)rows * nh * hd * 4, "q"));
-    CHECK(check_span(c, out, (uint64_t)rows * nh * hd * 4, "out"));
-    CHECK(check_span(c, kc, slots * kvd * esize(kv_type), "kc"));
-    CHECK(check_span(c, vc, slots * kvd * esize(kv_type), "vc"));
+    CHECK(check_span(c, q, sat_mul(sat_mul(rows, nh), (uint64_t)hd * 4), "q"));
+    CHECK(check_span(c, out, sat_mul(sat_mul(rows, nh), (uint64_t)hd * 4), "out"));
+    CHECK(check_span(c, kc, sat_mul(slots, kvd * esize(kv_type)), "kc"));
+    CHECK(check_span(c, vc, sat_mul(slots, kvd * esize(kv_type)), "vc"));
     const uint64_t row_bytes = kvd * esize(kv_type);
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / row_bytes;
     AttnCall a{q, kc, vc, kv_type, out, masks, tree ? 1u : 0u, rows, nh, nkv, hd, pos, scale, limit};
@@ -610,12 +633,12 @@ static int fused_step(bchip_ctx* c, Workspace& ws, float* q, const float* k, con
         return fail(BCHIP_E_ARG, "q, k, v, out and the caches must be 16-byte aligned");
     if ((uint64_t)pos + 1 > 0xffffffffull) return fail(BCHIP_E_ARG, "position past 2^32");
     const uint64_t kvd = (uint64_t)nkv * hd, slots = (uint64_t)pos + 1;
-    CHECK(check_span(c, q, (uint64_t)nh * hd * 4, "q"));
-    CHECK(check_span(c, out, (uint64_t)nh * hd * 4, "out"));
+    CHECK(check_span(c, q, sat_mul(nh, (uint64_t)hd * 4), "q"));
+    CHECK(check_span(c, out, sat_mul(nh, (uint64_t)hd * 4), "out"));
     CHECK(check_span(c, k, kvd * 4, "k"));
     CHECK(check_span(c, v, kvd * 4, "v"));
-    CHECK(check_span(c, kc, slots * kvd * esize(kv_type), "kc"));
-    CHECK(check_span(c, vc, slots * kvd * esize(kv_type), "vc"));
+    CHECK(check_span(c, kc, sat_mul(slots, kvd * esize(kv_type)), "kc"));
+    CHECK(check_span(c, vc, sat_mul(slots, kvd * esize(kv_type)), "vc"));
     CHECK(check_span(c, positions, 4, "positions"));
     CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
     if (ws.fixed && kv_type == BCHIP_F16) {
@@ -676,7 +699,7 @@ static int check_ragged(bchip_ctx* c, const void* kc, const void* vc, uint32_t k
     if (nseq > 256) return fail(BCHIP_E_ARG, "%u sequences (at most 256)", nseq);
     for (uint32_t i = 0; i < nseq; i++) {
         if (seq_lens[i] == 0) return fail(BCHIP_E_ARG, "sequence %u sees no slots", i);
-        const uint64_t end = (kv_offsets[i] + seq_lens[i]) * kvd * esize(kv_type);
+        const uint64_t end = sat_mul(sat_mul(sat_add(kv_offsets[i], seq_lens[i]), kvd), esize(kv_type));
         CHECK(check_span(c, kc, end, "kc"));
         CHECK(check_span(c, vc, end, "vc"));
     }
@@ -736,8 +759,8 @@ int bchip_attention_ragged(bchip_ctx* c, const float* q, const void* kc, const v
     if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc))
         return fail(BCHIP_E_ARG, "q, out and the caches must be 16-byte aligned");
     const uint64_t kvd = (uint64_t)nkv * hd;
-    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
-    CHECK(check_span(c, out, (uint64_t)nseq * nh * hd * 4, "out"));
+    CHECK(check_span(c, q, sat_mul(sat_mul(nseq, nh), (uint64_t)hd * 4), "q"));
+    CHECK(check_span(c, out, sat_mul(sat_mul(nseq, nh), (uint64_t)hd * 4), "out"));
     CHECK(check_ragged(c, kc, vc, kv_type, seq_lens, kv_offsets, nseq, kvd));
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
     AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, 0u, scale, limit};
@@ -757,9 +780,9 @@ int bchip_rope_append_ragged(bchip_ctx* c, float* q, const float* k, const float
     if (hd % 2 || rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
     if (nh == 0 || nkv == 0) return fail(BCHIP_E_ARG, "no heads");
     const uint64_t kvd = (uint64_t)nkv * hd;
-    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
-    CHECK(check_span(c, k, nseq * kvd * 4, "k"));
-    CHECK(check_span(c, v, nseq * kvd * 4, "v"));
+    CHECK(check_span(c, q, sat_mul(sat_mul(nseq, nh), (uint64_t)hd * 4), "q"));
+    CHECK(check_span(c, k, sat_mul(nseq, kvd * 4), "k"));
+    CHECK(check_span(c, v, sat_mul(nseq, kvd * 4), "v"));
     CHECK(check_span(c, positions, (uint64_t)nseq * 4, "positions"));
     CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
     CHECK(check_ragged(c, kc, vc, kv_type, seq_lens, kv_offsets, nseq, kvd));
@@ -787,10 +810,10 @@ int bchip_rope_append_attention_ragged(bchip_ctx* c, float* q, const float* k, c
     if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc) || (fuse && (!aligned16(k) || !aligned16(v))))
         return fail(BCHIP_E_ARG, "q, k, v, out and the caches must be 16-byte aligned");
     const uint64_t kvd = (uint64_t)nkv * hd;
-    CHECK(check_span(c, q, (uint64_t)nseq * nh * hd * 4, "q"));
-    CHECK(check_span(c, out, (uint64_t)nseq * nh * hd * 4, "out"));
-    CHECK(check_span(c, k, nseq * kvd * 4, "k"));
-    CHECK(check_span(c, v, nseq * kvd * 4, "v"));
+    CHECK(check_span(c, q, sat_mul(sat_mul(nseq, nh), (uint64_t)hd * 4), "q"));
+    CHECK(check_span(c, out, sat_mul(sat_mul(nseq, nh), (uint64_t)hd * 4), "out"));
+    CHECK(check_span(c, k, sat_mul(nseq, kvd * 4), "k"));
+    CHECK(check_span(c, v, sat_mul(nseq, kvd * 4), "v"));
     CHECK(check_span(c, positions, (uint64_t)nseq * 4, "positions"));
     CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
     CHECK(check_ragged(c, kc, vc, kv_type, seq_lens, kv_offsets, nseq, kvd));
@@ -831,7 +854,7 @@ int bchip_sample(bchip_ctx* c, const float* scores, uint32_t rows, uint32_t voca
     if (!scores || !ids) return fail(BCHIP_E_ARG, "null pointer");
     if (vocab == 0) return fail(BCHIP_E_ARG, "an empty vocabulary");
     if (rows > 65535) return fail(BCHIP_E_ARG, "%u rows (at most 65535 a call)", rows);
-    CHECK(check_span(c, scores, (uint64_t)rows * vocab * 4, "scores"));
+    CHECK(check_span(c, scores, sat_mul(rows, (uint64_t)vocab * 4), "scores"));
     CHECK(check_span(c, ids, (uint64_t)rows * 4, "ids"));
     size_t need = 0;
     if (temperature > 0.0f) {
@@ -849,7 +872,7 @@ int bchip_fill_normal(bchip_ctx* c, void* dst, uint32_t type, uint64_t n, uint64
     if (n == 0) return BCHIP_OK;
     if (!dst) return fail(BCHIP_E_ARG, "null pointer");
     if (type > 1) return fail(BCHIP_E_ARG, "element type %u", type);
-    CHECK(check_span(c, dst, n * esize(type), "fill"));
+    CHECK(check_span(c, dst, sat_mul(n, esize(type)), "fill"));
     HIP_TRY(fill_normal_launch(dst, type, n, seed, c->stream), "fill_normal");
     return BCHIP_OK;
 }

@@ -96,7 +96,7 @@ class _Cursor:
     def string(self) -> str:
         n = self.u64()
         if n > 1 << 24:
-            raise ValueError(f"a {n}-byte string in a GGUF header")
+            raise ValueError(f"GGUF header string of {n} bytes is past the limit")
         return self.take(n).decode("utf-8", errors="replace")
 
     def value(self, ty: int, depth: int):
@@ -121,10 +121,10 @@ class _Cursor:
             return self.string()
         if ty == 9:
             if depth > 2:
-                raise ValueError("nested arrays in a GGUF header")
+                raise ValueError("GGUF metadata array holds arrays (not accepted)")
             item, n = self.u32(), self.u64()
             if n > 1 << 24:
-                raise ValueError(f"an array of {n} items in a GGUF header")
+                raise ValueError(f"GGUF metadata array of {n} items is past the limit")
             return [self.value(item, depth + 1) for _ in range(n)]
         if ty == 10:
             return self.u64()
@@ -132,20 +132,20 @@ class _Cursor:
             return struct.unpack("<q", self.take(8))[0]
         if ty == 12:
             return struct.unpack("<d", self.take(8))[0]
-        raise ValueError(f"unknown GGUF value type {ty}")
+        raise ValueError(f"GGUF metadata value type {ty} is not defined")
 
 
 def parse(data: bytes) -> Header:
     """gguf.rs:157-200: the header from the start of a file."""
     c = _Cursor(bytes(data))
     if c.take(4) != b"GGUF":
-        raise ValueError("not a GGUF file")
+        raise ValueError("bad magic: the bytes do not start a GGUF container")
     version = c.u32()
     if version not in (2, 3):
-        raise ValueError(f"GGUF version {version} is not supported")
+        raise ValueError(f"GGUF container version {version} (2 and 3 are read)")
     n_tensors, n_meta = c.u64(), c.u64()
     if n_tensors > 1 << 20 or n_meta > 1 << 20:
-        raise ValueError(f"implausible GGUF header ({n_tensors} tensors, {n_meta} keys)")
+        raise ValueError(f"GGUF counts past the limits: {n_tensors} tensors, {n_meta} metadata keys")
     meta = {}
     for _ in range(n_meta):
         key = c.string()
@@ -155,7 +155,7 @@ def parse(data: bytes) -> Header:
         name = c.string()
         nd = c.u32()
         if nd > 4:
-            raise ValueError(f"tensor {name} has {nd} dimensions")
+            raise ValueError(f"tensor {name}: {nd} dimensions is past the limit")
         dims = [c.u64() for _ in range(nd)]
         raw.append((name, dims, c.u32(), c.u64()))
     align = meta.get("general.alignment")
@@ -164,13 +164,13 @@ def parse(data: bytes) -> Header:
     tensors = []
     for name, dims, ty, offset in raw:
         if ty not in BLOCKS:
-            raise ValueError(f"tensor {name}: ggml type {ty}")
+            raise ValueError(f"tensor {name}: ggml type {ty} is not one this loader reads")
         n, size = BLOCKS[ty]
         elements = 1
         for d in dims:
             elements *= d
         if elements % n:
-            raise ValueError(f"tensor {name}: {elements} weights are not whole blocks of {n}")
+            raise ValueError(f"tensor {name}: {elements} elements do not fill whole {n}-weight blocks")
         start = data_start + offset
         tensors.append(TensorInfo(name, dims, ty, (start, start + elements // n * size)))
     return Header(version, meta, tensors, data_start)
@@ -220,7 +220,7 @@ def config_from_header(h: Header) -> Config:
     """Config::from_header (model.rs:44-70)."""
     arch = h.arch()
     if arch not in ("llama", "qwen2", "mistral"):
-        raise ValueError(f"the {arch} architecture is not supported yet (llama and qwen2 are)")
+        raise ValueError(f"model architecture {arch!r}: only llama, mistral and qwen2 layouts load")
 
     def need(key):
         v = h.arch_u64(key)

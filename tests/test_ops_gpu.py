@@ -127,3 +127,41 @@ def test_fill_normal_is_the_oracle_generator(ctx):
     np.testing.assert_allclose(got, want, rtol=2e-7, atol=1e-7)
     assert (got == want).mean() > 0.99
     b.free()
+
+
+def test_offsets_that_overflow_are_refused_before_any_launch(ctx):
+    """Slot offsets whose byte spans overflow 64 bits, or wrap the address space, must fail the
+    argument checks (BCHIP_E_ARG) rather than wrap into a span that passes them. Nothing is
+    launched: each call is refused on the host."""
+    nh, nkv, hd, rd = 4, 2, 64, 64
+    kvd = nkv * hd
+    q, k, v = rand((2, nh * hd), 11), rand((2, kvd), 12), rand((2, kvd), 13)
+    qb, kb, vb = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    kc, vc = ctx.zeros(64 * kvd * 2), ctx.zeros(64 * kvd * 2)
+    ib = ctx.upload(O.inv_freq(rd, 1e4))
+    pb = ctx.upload(np.array([5, 6], np.uint32))
+    out = ctx.zeros(2 * nh * hd * 4)
+    # (offset + rows) * kvd * 2 wraps to a small number for these offsets.
+    wraps = [(1 << 64) // (kvd * 2) - 1, (1 << 63) + 1, (1 << 64) - 2]
+
+    def refused(fn):
+        with pytest.raises(bchip.BchipError) as e:
+            fn()
+        assert e.value.code == bchip.E_ARG, bchip.last_error()
+
+    for off in wraps:
+        refused(lambda: ctx.rope_append(qb, kb, vb, kc, vc, bchip.F16, ib, pb, 1, nh, nkv, hd, rd, True, off))
+        refused(lambda: ctx.rope_append_ragged(qb, kb, vb, kc, vc, bchip.F16, ib, pb, [3], [off], nh, nkv, hd, rd,
+                                               True))
+        refused(lambda: ctx.rope_append_attention_ragged(qb, kb, vb, kc, vc, bchip.F16, ib, pb, [3], [off], nh, nkv,
+                                                         hd, rd, True, 0.125, out))
+        refused(lambda: ctx.attention_ragged(qb, kc, vc, bchip.F16, out, [3], [off], nh, nkv, hd, 0.125))
+        refused(lambda: ctx.copy(kb, bchip.F32, kc, bchip.F16, off, 8))
+        refused(lambda: ctx.move(kc, bchip.F16, off, 0, 8))
+        refused(lambda: ctx.fill_normal(kc, bchip.F16, off, 1))
+    with pytest.raises(bchip.BchipError):
+        ctx.read(kc, (4,), np.float16, off=(1 << 64) - 4)
+    # The caches are untouched: every call above was refused before it launched anything.
+    np.testing.assert_array_equal(ctx.read(kc, (64 * kvd,), np.float16), 0)
+    for b in (qb, kb, vb, kc, vc, ib, pb, out):
+        b.free()
