@@ -1374,6 +1374,207 @@ __device__ __forceinline__ void tile_softmax(State<NDT>& s, const f32x4 (&x)[4],
         pb[kc] = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
 }
 
+// ---------------------------------------------------------------------------------------
+// Single-launch fold of split chunks (group fold). A split launch's workgroups of one group
+// (one KV head's row block) each compute one chunk's state. Instead of a second kernel
+// (attn_combine) that starts once the whole launch has drained, every workgroup publishes its
+// state, counts itself in at the group's arrival counter, waits until the group's nchunk
+// workgroups are all in, and then folds one slice of the group's outputs over all the chunks:
+// the same left fold, in chunk order, with attn_combine's expressions, so the outputs are the
+// same bits.
+// Where the states travel: each XCD has its own L2, and another XCD sees a plain store only
+// after that L2 is written back. The launch places a group's workgroups on one XCD when it
+// can (workgroups go to the XCDs in turn, so block indices 8 apart share one), and each
+// workgroup records the XCD it runs on (its XCC_ID) in the group's mask. A group found on one
+// XCD exchanges its states through that XCD's L2: plain stores, plain loads. A group spread
+// over several (a different dispatch order, a device in another partition mode) publishes
+// every state again with write-through stores, counts in a second time, and reads them after
+// an agent-scope acquire; its results are the same bits, only later.
+// The host takes this path only when every workgroup of the launch can be resident at once
+// (one a CU, at most as many as the device has CUs), so a waiting workgroup never holds a CU
+// that another of its group needs. The waits are bounded all the same: if other work holds
+// the GPU past the bound, the workgroup stops waiting, writes NaN for its outputs and sets the
+// context's error word, which bchip_sync reports.
+// Per group, GROUP_STRIDE words at gcnt + grp * GROUP_STRIDE: a 64-bit arrival word (the
+// count in bits 0-15, the sum of the arrivals' XCC_IDs in bits 16-31 and the sum of their
+// squares in bits 32-63: one poll tells both that all are in and whether all ran on one XCD,
+// as n * sum(x^2) == sum(x)^2 exactly when every x is the same), the second arrivals, and the
+// departures; the last workgroup to leave clears them for the next call.
+constexpr uint32_t GFOLD_MAX_CHUNKS = 32;
+constexpr uint32_t GFOLD_SPINS = 1u << 16;  // each a counter read and ~128 clocks of sleep
+enum : uint32_t { GS_ARRIVE = 0, GS_ARRIVE2 = 2, GS_LEAVE = 3 };
+enum : uint32_t { GF_TIMEOUT = 0, GF_LOCAL = 1, GF_SPREAD = 2 };
+
+// A store that writes through to device memory (agent-scope coherence): once this wave's
+// vmcnt has drained it is visible to agent-scope loads from any XCD, with no L2 write-back.
+__device__ __forceinline__ void store_wt4(float* p, f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_wt2(float* p, float a, float b) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(f32x2{a, b}) : "memory");
+}
+
+// The XCD this wave runs on (HW_REG_XCC_ID, bits 3:0).
+__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)); }
+
+// A workgroup's side of its group's synchronisation, carried from the arrival to the
+// departure. Thread 0 arrives and waits; the workgroup's last thread counts it out (a lane
+// with no fold work at verify sizes, so that the count's round trip, which its wave's later
+// loads would wait behind, holds up none of the fold's loads).
+struct GroupSync {
+    uint32_t* gs;
+    uint32_t n;
+    uint32_t leave_old;  // the last thread: the departure count before this workgroup's
+};
+
+__device__ __forceinline__ void group_depart(GroupSync& s) {
+    if (threadIdx.x == blockDim.x - 1)
+        s.leave_old = __hip_atomic_fetch_add(s.gs + GS_LEAVE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread once the workgroup's state is stored (plain stores). Returns
+// GF_LOCAL (the group ran on one XCD: the states are in its L2; the workgroup has counted
+// itself out, nothing later waits on the group's words), GF_SPREAD (the caller must publish
+// its state again write-through and call group_second), or GF_TIMEOUT. flag: an LDS word
+// the workgroup no longer uses (the kernels' LDS is full).
+__device__ __forceinline__ uint32_t group_arrive(GroupSync& s, uint32_t* err, uint32_t& flag) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t* word = (uint64_t*)(s.gs + GS_ARRIVE);
+        const uint64_t x = xcc_id();
+        __hip_atomic_fetch_add(word, 1ull | (x << 16) | (x * x << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t mode = GF_TIMEOUT;
+        uint64_t v = 0;
+        for (uint32_t spins = 0;; spins++) {
+            v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((uint32_t)(v & 0xffff) >= s.n || spins == GFOLD_SPINS) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if ((uint32_t)(v & 0xffff) >= s.n) {
+            const uint64_t sx = (v >> 16) & 0xffff, sxx = v >> 32;
+            mode = (uint64_t)s.n * sxx == sx * sx ? GF_LOCAL : GF_SPREAD;
+            // This CU's L1 holds nothing of other workgroups' states; drop it all the same.
+            if (mode == GF_LOCAL) asm volatile("buffer_inv sc0" ::: "memory");
+        } else {
+            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        flag = mode;
+    }
+    __syncthreads();
+    const uint32_t mode = flag;
+    if (mode == GF_LOCAL) group_depart(s);
+    return mode;
+}
+
+// A spread group, after the caller stored its state again write-through: the second count,
+// the departure, then an agent-scope acquire (this CU's L1 and this XCD's L2 drop what they
+// hold of other XCDs' writes). Returns GF_SPREAD or GF_TIMEOUT.
+__device__ __forceinline__ uint32_t group_second(GroupSync& s, uint32_t* err, uint32_t& flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t* w = s.gs + GS_ARRIVE2;
+        __hip_atomic_fetch_add(w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t spins = 0;
+        while (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < s.n && ++spins < GFOLD_SPINS)
+            __builtin_amdgcn_s_sleep(2);
+        const bool ok = spins < GFOLD_SPINS;
+        if (!ok) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        flag = ok ? GF_SPREAD : GF_TIMEOUT;
+    }
+    __syncthreads();
+    const uint32_t mode = flag;
+    if (mode == GF_SPREAD) group_depart(s);
+    return mode;
+}
+
+// Thread 0 of the last workgroup to have counted itself out clears the group's words for the
+// next call (every workgroup of the group had passed every wait when it counted out).
+__device__ __forceinline__ void group_leave(const GroupSync& s) {
+    if (threadIdx.x == blockDim.x - 1 && s.leave_old == s.n - 1) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) __hip_atomic_store(s.gs + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Workgroup cs_idx's share of group grp's outputs: slots cs_idx * per .. (per = SL / nchunk,
+// rounded up), one slot a wave at a time, two dims a lane. Each output is attn_combine's fold
+// over the group's chunk states in chunk order. Its weights depend only on the running maxima,
+// which are the prefix maxima of the chunks' maxima (a max is exact in any order): lane c
+// takes chunk c's max and sum, a scan across lanes gives the maximum of the chunks before it,
+// and lane c computes chunk c's pair of weights from the same operands as the serial fold.
+// The sum and the two dims then run the serial recurrence, every lane reading each chunk's
+// weights and sum back from LDS (wts: GFOLD_MAX_CHUNKS float4 a wave, LDS the workgroup no
+// longer uses), so every product and sum is the serial fold's, in its order.
+template <int SL>
+__device__ __forceinline__ void group_fold_slots(const SharedParams& p, uint32_t grp, uint32_t cs_idx, uint32_t rbi,
+                                                 uint32_t kvh, bool ok, float4* wts) {
+    constexpr uint32_t HD = 128, MC = GFOLD_MAX_CHUNKS;
+    static_assert(MC <= 32, "a chunk's weights sit in lanes 0..31");
+    const uint32_t nch = p.nchunk;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint32_t per = (SL + nch - 1) / nch;
+    const uint32_t lo = cs_idx * per, hi = min(lo + per, (uint32_t)SL);
+    for (uint32_t slot = lo + wave; slot < hi; slot += nw) {
+        const uint32_t gh = slot / p.rb, r = rbi * p.rb + slot % p.rb;
+        if (gh >= p.G || r >= p.rows) continue;
+        float* dst = p.out + ((size_t)r * p.nh + kvh * p.G + gh) * HD + 2 * lane;
+        if (!ok) {
+            const float qnan = __uint_as_float(0x7fc00000u);  // a bit pattern: this object has no NaN arithmetic
+            *(float2*)dst = float2{qnan, qnan};
+            continue;
+        }
+        // The states of a group fold sit as [group][slot][chunk][HD], a slot's chunks 512 bytes
+        // apart, and the workspace holds GFOLD_MAX_CHUNKS chunk states past the last group's:
+        // every load is unconditional and off one base (chunks past the group's last read
+        // whatever follows, unused). A load behind a branch would make the compiler wait for
+        // all loads in flight where it joins.
+        const size_t sbase = ((size_t)grp * SL + slot) * nch;
+        const float2 ml = *(const float2*)(p.part_ml + (sbase + (lane & (MC - 1))) * 2);
+        const float* ob = p.part_o + sbase * HD + 2 * lane;
+        float2 o[MC];
+#pragma unroll
+        for (uint32_t c = 0; c < MC; c++) o[c] = *(const float2*)(ob + c * HD);
+        const float mc = lane < nch ? ml.x : -INFINITY;
+        float pm = mc;  // inclusive prefix max over lanes 0..31
+#pragma unroll
+        for (int d = 1; d < 32; d <<= 1) {
+            const float t = __shfl_up(pm, d);
+            if (lane >= (uint32_t)d) pm = fmaxf(pm, t);
+        }
+        float before = __shfl_up(pm, 1);  // the running max before chunk `lane`
+        if (lane == 0) before = -INFINITY;
+        float a, b, mn;
+        merge_coef(before, mc, a, b, mn);
+        float4* wl = wts + wave * MC;
+        if (lane < MC) wl[lane] = float4{a, b, ml.y, 0.0f};
+        float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+        // Eight chunks' weights a read batch (one address for the whole wave: broadcast
+        // reads), then eight steps, each a uniform branch the compiler keeps.
+#pragma unroll
+        for (uint32_t c0 = 0; c0 < MC; c0 += 8) {
+            if (c0 >= nch) break;
+            float4 wc[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) wc[j] = wl[c0 + j];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) {
+                if (c0 + j < nch) {
+                    keep_branch();
+                    L = L * wc[j].x + wc[j].z * wc[j].y;
+                    O0 = O0 * wc[j].x + o[c0 + j].x * wc[j].y;
+                    O1 = O1 * wc[j].x + o[c0 + j].y * wc[j].y;
+                }
+            }
+        }
+        *(float2*)dst = float2{O0 / L, O1 / L};
+    }
+}
+
 // The prefill kernel proper: one 16-slot tile per wave, W waves sharing each K and V block
 // in LDS, block_step's arithmetic per slot. Blocks stream through a ring of three LDS
 // stages (one LDS object each, K then V), one chunk's worth, fetched two blocks ahead by
@@ -1421,8 +1622,19 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, n = lane & 15;
-    const uint32_t gi_launch = p.split ? blockIdx.x / p.nchunk : blockIdx.x;
-    const uint32_t cs_idx = p.split ? blockIdx.x % p.nchunk : 0u;
+    // Split launches: block -> (group in launch order, chunk). With xmap, blocks 8 apart (one
+    // XCD's share when workgroups go to the XCDs in turn) take one group's chunks.
+    uint32_t gi_launch = blockIdx.x, cs_idx = 0;
+    if (p.split) {
+        if (p.xmap) {
+            const uint32_t x = blockIdx.x % 8u, k = blockIdx.x / 8u;
+            gi_launch = x + 8u * (k / p.nchunk);
+            cs_idx = k % p.nchunk;
+        } else {
+            gi_launch = blockIdx.x / p.nchunk;
+            cs_idx = blockIdx.x % p.nchunk;
+        }
+    }
     const uint32_t kvh = gi_launch % p.nkv;
     const uint32_t rbi = p.nrb - 1u - gi_launch / p.nkv;  // heaviest row blocks first
     const uint32_t grp = kvh * p.nrb + rbi;
@@ -1671,15 +1883,33 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         }
     }
     if (p.split) {
-        const size_t u = (size_t)grp * p.nchunk + cs_idx;
+        // The chunk's state: [unit][slot][HD] for attn_combine, [group][slot][chunk][HD] for
+        // the group fold (a slot's chunks together).
         const uint32_t sl = 16 * w + n;
-        float* po = p.part_o + (u * (16 * W) + sl) * HD;
+        const size_t at = p.gcnt ? ((size_t)grp * (16 * W) + sl) * p.nchunk + cs_idx
+                                 : ((size_t)grp * p.nchunk + cs_idx) * (16 * W) + sl;
+        float* po = p.part_o + at * HD;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             const uint32_t d = 16 * dt + 4 * g;
             *(float4*)(po + d) = float4{cs.o[dt][0], cs.o[dt][1], cs.o[dt][2], cs.o[dt][3]};
         }
-        if (g == 0) *(float2*)(p.part_ml + (u * (16 * W) + sl) * 2) = float2{cs.m, cs.l};
+        if (g == 0) *(float2*)(p.part_ml + at * 2) = float2{cs.m, cs.l};
+        if (!p.gcnt) return;  // attn_combine folds the states
+        // Group fold. Q's LDS rows are free for the flag word: each wave read its own rows
+        // before its first block.
+        GroupSync gsync{p.gcnt + (size_t)grp * GROUP_STRIDE, p.nchunk, 0u};
+        uint32_t& flag = *(uint32_t*)&qlds[0][0];
+        uint32_t mode = group_arrive(gsync, p.gerr, flag);
+        if (mode == GF_SPREAD) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) store_wt4(po + 16 * dt + 4 * g, cs.o[dt]);
+            if (g == 0) store_wt2(p.part_ml + at * 2, cs.m, cs.l);
+            mode = group_second(gsync, p.gerr, flag);
+        }
+        // The ring's first stage is free: every wave is past its last block.
+        group_fold_slots<16 * W>(p, grp, cs_idx, rbi, kvh, mode != GF_TIMEOUT, (float4*)ring0);
+        if (mode != GF_TIMEOUT) group_leave(gsync);
         return;
     }
     fold(R, cs);
@@ -2216,12 +2446,24 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     const uint32_t groups = a.nkv * sp.nrb;
     sp.split = groups < 512 && sp.nchunk > 1;
     if (sp.split) {
-        hipError_t e = ws.reserve((size_t)groups * sp.nchunk * SL, (size_t)hdp);
+        // (GFOLD_MAX_CHUNKS states to spare past the last: the group fold's loads run past a
+        // slot's last chunk.)
+        hipError_t e = ws.reserve((size_t)groups * sp.nchunk * SL + GFOLD_MAX_CHUNKS, (size_t)hdp);
         if (e != hipSuccess) return e;
         sp.part_o = ws.o;
         sp.part_ml = ws.ml;
     }
     const uint32_t blocks = groups * (sp.split ? sp.nchunk : 1u);
+    // The group fold (see group_arrive_wait) for split passes of the f16 hd-128 kernels whose
+    // workgroups can all be resident at once: one a CU (their LDS takes most of one), at most
+    // the device's CU count.
+    const bool gfold = sp.split && a.kv_type == 1 && a.hd == 128 && ws.group_fold && ws.gcnt && blocks <= ws.cus &&
+                       sp.nchunk <= GFOLD_MAX_CHUNKS && groups <= GROUP_COUNTERS;
+    if (gfold) {
+        sp.gcnt = ws.gcnt;
+        sp.gerr = ws.gerr;
+        sp.xmap = groups % 8 == 0;  // each XCD's share of blocks then holds whole groups
+    }
     hipError_t e;
     if (a.kv_type == 1 && a.hd == 128) {
         // Many rows re-read every V block many times: transpose V once (a pass over V) so
@@ -2264,7 +2506,7 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     } else {
         return hipErrorInvalidValue;  // f32 caches take the f32 path (attention_f32.hip)
     }
-    if (e != hipSuccess || !sp.split) return e;
+    if (e != hipSuccess || !sp.split || gfold) return e;
     CombineParams cp{};
     cp.zero = ws.zero;
     cp.out = a.out;

@@ -86,6 +86,20 @@ int enter(bchip_ctx* c) {
     return BCHIP_OK;
 }
 
+// After the stream has drained: a single-launch fold whose wait for the other workgroups of
+// its group ran out (other work held the CUs they needed) wrote NaN for its outputs and set
+// the error word. Reported once, then cleared.
+int fold_status(bchip_ctx* c) {
+    if (c->ws.gerr_host && *c->ws.gerr_host) {
+        *c->ws.gerr_host = 0;
+        // The stream has drained: no fold is waiting, so the counters can start over.
+        (void)hipMemset(c->ws.gcnt, 0, (size_t)GROUP_COUNTERS * GROUP_STRIDE * sizeof(uint32_t));
+        return fail(BCHIP_E_HIP, "an attention fold timed out waiting for its workgroups (other kernels held "
+                                 "the GPU); that call's outputs are NaN");
+    }
+    return BCHIP_OK;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Byte counts from element counts, saturated: a count that overflows 64 bits becomes
@@ -157,7 +171,7 @@ int check_heads(uint32_t nh, uint32_t nkv, uint32_t hd) {
 
 namespace bchip {
 
-void Workspace::set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_bytes, void* zero_page) {
+void Workspace::set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_bytes, const Workspace& owner) {
     fixed = true;
     o = (float*)base;
     ml = (float*)((char*)base + o_bytes);
@@ -165,7 +179,12 @@ void Workspace::set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_
     o_cap = o_bytes;
     ml_cap = ml_bytes;
     qrot_cap = q_bytes;
-    zero = zero_page;
+    zero = owner.zero;
+    gcnt = owner.gcnt;
+    cus = owner.cus;
+    group_fold = owner.group_fold;
+    gerr = owner.gerr;
+    gerr_host = owner.gerr_host;
 }
 
 hipError_t Workspace::reserve(size_t need_slots, size_t hd_pad) {
@@ -219,10 +238,26 @@ hipError_t Workspace::reserve_qrot(size_t floats) {
     return hipSuccess;
 }
 
-hipError_t Workspace::init() {
+hipError_t Workspace::init(int device) {
     hipError_t e = hipMalloc(&zero, ZERO_BYTES);
-    if (e != hipSuccess) return e;
-    return hipMemset(zero, 0, ZERO_BYTES);
+    if (e == hipSuccess) e = hipMemset(zero, 0, ZERO_BYTES);
+    if (e == hipSuccess) e = hipMalloc((void**)&gcnt, (size_t)GROUP_COUNTERS * GROUP_STRIDE * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(gcnt, 0, (size_t)GROUP_COUNTERS * GROUP_STRIDE * sizeof(uint32_t));
+    int n = 0;
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+    cus = n > 0 ? (uint32_t)n : 0u;
+    // A caller whose GPU runs other kernels beside this library's can turn the single-launch
+    // folds off (their workgroups wait for each other; see attention.hip).
+    const char* gf = getenv("BCHIP_GROUP_FOLD");
+    group_fold = !(gf && strcmp(gf, "0") == 0);
+    void* h = nullptr;
+    if (e == hipSuccess) e = hipHostMalloc(&h, 64, hipHostMallocMapped);
+    if (e == hipSuccess) {
+        gerr_host = (volatile uint32_t*)h;
+        *gerr_host = 0;
+        e = hipHostGetDevicePointer((void**)&gerr, h, 0);
+    }
+    return e;
 }
 
 void Workspace::release() {
@@ -266,12 +301,12 @@ int bchip_init(int device, bchip_ctx** out) {
     c->name = std::string(prop.name[0] ? prop.name : prop.gcnArchName) + " (" +
               std::to_string(prop.multiProcessorCount) + " CUs)";
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-    if (e == hipSuccess) e = c->ws.init();
+    if (e == hipSuccess) e = c->ws.init(device);
     if (e == hipSuccess) {
         // This device's copy of the no-allocation scratch (the device is current here).
         void* sp = nullptr;
         e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
-        if (e == hipSuccess) c->fixed_ws.set_fixed(sp, NOALLOC_O_BYTES, NOALLOC_ML_BYTES, NOALLOC_Q_BYTES, c->ws.zero);
+        if (e == hipSuccess) c->fixed_ws.set_fixed(sp, NOALLOC_O_BYTES, NOALLOC_ML_BYTES, NOALLOC_Q_BYTES, c->ws);
     }
     if (e == hipSuccess) e = hipMalloc((void**)&c->mm_cnt, MATMUL_COUNTERS * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->mm_cnt, 0, MATMUL_COUNTERS * sizeof(uint32_t));
@@ -291,6 +326,8 @@ int bchip_destroy(bchip_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     c->ws.release();
     if (c->ws.zero) (void)hipFree(c->ws.zero);
+    if (c->ws.gcnt) (void)hipFree(c->ws.gcnt);
+    if (c->ws.gerr_host) (void)hipHostFree((void*)c->ws.gerr_host);
     if (c->mm_cnt) (void)hipFree(c->mm_cnt);
     for (auto& a : c->allocs) (void)hipFree((void*)a.first);
     if (c->t0) (void)hipEventDestroy(c->t0);
@@ -369,13 +406,13 @@ int bchip_download(bchip_ctx* c, const void* dev, size_t off, void* host, size_t
     CHECK(check_at(c, dev, off, bytes, "download"));
     HIP_TRY(hipMemcpyAsync(host, (const char*)dev + off, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    return BCHIP_OK;
+    return fold_status(c);
 }
 
 int bchip_sync(bchip_ctx* c) {
     CHECK(enter(c));
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    return BCHIP_OK;
+    return fold_status(c);
 }
 
 int bchip_stream(bchip_ctx* c, void** s) {

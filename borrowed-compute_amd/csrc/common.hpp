@@ -156,6 +156,13 @@ struct SharedParams {
     uint32_t nrb;   // row blocks
     uint32_t nchunk;// chunks of the longest list (split launches)
     uint32_t split;
+    // Split launches folded in the same launch (group fold): each workgroup publishes its
+    // chunk state, waits at its group's arrival counter gcnt[grp * GROUP_STRIDE] for the
+    // group's other nchunk - 1 workgroups, then folds one slice of the group's outputs.
+    // Null: the states go to attn_combine instead. gerr: the word a wait that runs out sets.
+    uint32_t* gcnt;
+    uint32_t* gerr;
+    uint32_t xmap;  // split launches: blocks 8 apart take one group's chunks (one XCD each)
 };
 
 struct CombineParams {

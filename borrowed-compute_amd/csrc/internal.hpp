@@ -16,15 +16,24 @@ struct Workspace {
     float* o = nullptr;    // [units*slots][hd_pad]: chunk states
     float* ml = nullptr;   // [units*slots][2]
     void* zero = nullptr;  // ZERO_BYTES of zeros
+    // Arrival counters of the single-launch folds (GROUP_COUNTERS, GROUP_STRIDE words apart,
+    // zero between calls), the device's CU count (how many one-CU workgroups can be resident
+    // at once), and a word in host memory that a fold whose wait ran out sets (never
+    // otherwise): bchip_sync reports it.
+    uint32_t* gcnt = nullptr;
+    uint32_t cus = 0;
+    bool group_fold = true;  // BCHIP_GROUP_FOLD=0 at init turns the single-launch folds off
+    uint32_t* gerr = nullptr;       // device address of the host word
+    volatile uint32_t* gerr_host = nullptr;
     void* vt = nullptr;    // V^T tiles of a prefill call; the sampler's keys and sort scratch
     float* qrot = nullptr;  // rotated q of a fused step, until attn_row_fold copies it
     size_t slots = 0, hdp = 0, vt_bytes = 0, qrot_floats = 0;
     bool fixed = false;
     size_t o_cap = 0, ml_cap = 0, qrot_cap = 0;  // fixed: bytes of o, ml and qrot
-    hipError_t init();     // allocates the zero page
-    // The fixed view: o, ml and qrot at base (o_bytes, ml_bytes, q_bytes each), the zero page
-    // of `zero_page`.
-    void set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_bytes, void* zero_page);
+    hipError_t init(int device);  // allocates the zero page, the counters and the error word
+    // The fixed view: o, ml and qrot at base (o_bytes, ml_bytes, q_bytes each); the zero page,
+    // counters and error word of `owner`.
+    void set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_bytes, const Workspace& owner);
     hipError_t reserve(size_t need_slots, size_t hd_pad);
     hipError_t reserve_qrot(size_t floats);
     hipError_t reserve_vt(size_t bytes);
@@ -32,6 +41,8 @@ struct Workspace {
 };
 
 constexpr size_t ZERO_BYTES = 4096;
+constexpr uint32_t GROUP_COUNTERS = 1024;
+constexpr uint32_t GROUP_STRIDE = 32;  // one 128-byte line a counter
 
 struct AttnCall {
     const float* q;
