@@ -1401,7 +1401,8 @@ __device__ __forceinline__ void tile_softmax(State<NDT>& s, const f32x4 (&x)[4],
 // as n * sum(x^2) == sum(x)^2 exactly when every x is the same), the second arrivals, and the
 // departures; the last workgroup to leave clears them for the next call.
 constexpr uint32_t GFOLD_MAX_CHUNKS = 32;
-constexpr uint32_t GFOLD_SPINS = 1u << 16;  // each a counter read and ~128 clocks of sleep
+// A wait takes at most SharedParams::gspins polls (2^16 unless a test lowers it), each a
+// counter read and ~128 clocks of sleep.
 enum : uint32_t { GS_ARRIVE = 0, GS_ARRIVE2 = 2, GS_LEAVE = 3 };
 enum : uint32_t { GF_TIMEOUT = 0, GF_LOCAL = 1, GF_SPREAD = 2 };
 
@@ -1425,6 +1426,8 @@ __device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg(
 struct GroupSync {
     uint32_t* gs;
     uint32_t n;
+    uint32_t spins;      // polls a wait may take
+    uint32_t spread;     // take the spread path whatever the XCDs
     uint32_t leave_old;  // the last thread: the departure count before this workgroup's
 };
 
@@ -1449,12 +1452,12 @@ __device__ __forceinline__ uint32_t group_arrive(GroupSync& s, uint32_t* err, ui
         uint64_t v = 0;
         for (uint32_t spins = 0;; spins++) {
             v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if ((uint32_t)(v & 0xffff) >= s.n || spins == GFOLD_SPINS) break;
+            if ((uint32_t)(v & 0xffff) >= s.n || spins == s.spins) break;
             __builtin_amdgcn_s_sleep(2);
         }
         if ((uint32_t)(v & 0xffff) >= s.n) {
             const uint64_t sx = (v >> 16) & 0xffff, sxx = v >> 32;
-            mode = (uint64_t)s.n * sxx == sx * sx ? GF_LOCAL : GF_SPREAD;
+            mode = (uint64_t)s.n * sxx == sx * sx && !s.spread ? GF_LOCAL : GF_SPREAD;
             // This CU's L1 holds nothing of other workgroups' states; drop it all the same.
             if (mode == GF_LOCAL) asm volatile("buffer_inv sc0" ::: "memory");
         } else {
@@ -1478,9 +1481,9 @@ __device__ __forceinline__ uint32_t group_second(GroupSync& s, uint32_t* err, ui
         uint32_t* w = s.gs + GS_ARRIVE2;
         __hip_atomic_fetch_add(w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t spins = 0;
-        while (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < s.n && ++spins < GFOLD_SPINS)
+        while (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < s.n && ++spins < s.spins)
             __builtin_amdgcn_s_sleep(2);
-        const bool ok = spins < GFOLD_SPINS;
+        const bool ok = spins < s.spins;
         if (!ok) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         flag = ok ? GF_SPREAD : GF_TIMEOUT;
@@ -1898,7 +1901,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         if (!p.gcnt) return;  // attn_combine folds the states
         // Group fold. Q's LDS rows are free for the flag word: each wave read its own rows
         // before its first block.
-        GroupSync gsync{p.gcnt + (size_t)grp * GROUP_STRIDE, p.nchunk, 0u};
+        GroupSync gsync{p.gcnt + (size_t)grp * GROUP_STRIDE, p.nchunk, p.gspins, p.gspread, 0u};
         uint32_t& flag = *(uint32_t*)&qlds[0][0];
         uint32_t mode = group_arrive(gsync, p.gerr, flag);
         if (mode == GF_SPREAD) {
@@ -2463,6 +2466,8 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
         sp.gcnt = ws.gcnt;
         sp.gerr = ws.gerr;
         sp.xmap = groups % 8 == 0;  // each XCD's share of blocks then holds whole groups
+        sp.gspread = ws.group_spread;
+        sp.gspins = ws.group_spins;
     }
     hipError_t e;
     if (a.kv_type == 1 && a.hd == 128) {

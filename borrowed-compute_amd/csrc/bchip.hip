@@ -183,6 +183,8 @@ void Workspace::set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_
     gcnt = owner.gcnt;
     cus = owner.cus;
     group_fold = owner.group_fold;
+    group_spread = owner.group_spread;
+    group_spins = owner.group_spins;
     gerr = owner.gerr;
     gerr_host = owner.gerr_host;
 }
@@ -250,6 +252,11 @@ hipError_t Workspace::init(int device) {
     // folds off (their workgroups wait for each other; see attention.hip).
     const char* gf = getenv("BCHIP_GROUP_FOLD");
     group_fold = !(gf && strcmp(gf, "0") == 0);
+    group_spread = gf && strcmp(gf, "spread") == 0;
+    if (const char* sp = getenv("BCHIP_GROUP_FOLD_SPINS")) {
+        const long v = strtol(sp, nullptr, 10);
+        if (v > 0 && v < (1l << 24)) group_spins = (uint32_t)v;
+    }
     void* h = nullptr;
     if (e == hipSuccess) e = hipHostMalloc(&h, 64, hipHostMallocMapped);
     if (e == hipSuccess) {

@@ -163,6 +163,8 @@ struct SharedParams {
     uint32_t* gcnt;
     uint32_t* gerr;
     uint32_t xmap;  // split launches: blocks 8 apart take one group's chunks (one XCD each)
+    uint32_t gspread;  // group fold: take the spread path whatever the XCDs (tests)
+    uint32_t gspins;   // group fold: polls a wait may take
 };
 
 struct CombineParams {

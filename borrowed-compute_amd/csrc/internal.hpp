@@ -22,7 +22,12 @@ struct Workspace {
     // otherwise): bchip_sync reports it.
     uint32_t* gcnt = nullptr;
     uint32_t cus = 0;
-    bool group_fold = true;  // BCHIP_GROUP_FOLD=0 at init turns the single-launch folds off
+    // BCHIP_GROUP_FOLD at init: 0 turns the single-launch folds off; "spread" makes every
+    // group take the path of a group spread over several XCDs (for tests of that path).
+    // BCHIP_GROUP_FOLD_SPINS bounds their waits (for tests of a wait that runs out).
+    bool group_fold = true;
+    uint32_t group_spread = 0;
+    uint32_t group_spins = 1u << 16;
     uint32_t* gerr = nullptr;       // device address of the host word
     volatile uint32_t* gerr_host = nullptr;
     void* vt = nullptr;    // V^T tiles of a prefill call; the sampler's keys and sort scratch

@@ -111,3 +111,76 @@ def test_group_counters_start_over_between_calls(ctxs):
         np.testing.assert_array_equal(one.read(out, (8, nh, hd)), alone[pos], err_msg=f"pos {pos}")
         out.free()
     p.free()
+
+
+def _ctx_with(env):
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return bchip.Ctx(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("rows,pos,nh,nkv,hd", [(8, 4096, 64, 8, 128), (100, 700, 28, 4, 128)])
+def test_spread_groups_give_the_same_bits(ctxs, rows, pos, nh, nkv, hd):
+    """The path of a group whose workgroups ran on several XCDs (each state published again
+    write-through, a second count, an agent-scope acquire), forced from the host: the same
+    bits as the two-launch fold."""
+    _, two = ctxs
+    spread = _ctx_with({"BCHIP_GROUP_FOLD": "spread"})
+    try:
+        n = pos + rows
+        q = rand((rows, nh, hd), rows + pos)
+        kc, vc = rand((n, nkv * hd), pos + 1), rand((n, nkv * hd), pos + 2)
+        a, b = Pass(spread, q, kc, vc, nh, nkv, hd), Pass(two, q, kc, vc, nh, nkv, hd)
+        for _ in range(3):  # and its counters start over between calls
+            np.testing.assert_array_equal(a.run(rows, pos), b.run(rows, pos))
+        a.free()
+        b.free()
+    finally:
+        spread.close()
+
+
+def test_a_wait_that_runs_out_is_reported_and_the_next_call_recovers(ctxs):
+    """A group fold whose bound on waiting runs out (forced from the host: a bound of one poll,
+    so workgroups that arrive before the last stop waiting) writes NaN for its outputs and sets
+    the context's error word: the next bchip_sync reports it, and a call after that, with the
+    counters cleared, is right again. Every kernel still exits normally."""
+    _, two = ctxs
+    short = _ctx_with({"BCHIP_GROUP_FOLD_SPINS": "1"})
+    try:
+        rows, pos, nh, nkv, hd = 8, 4096, 64, 8, 128
+        n = pos + rows
+        q = rand((rows, nh, hd), 9)
+        kc, vc = rand((n, nkv * hd), 10), rand((n, nkv * hd), 11)
+        a, b = Pass(short, q, kc, vc, nh, nkv, hd), Pass(two, q, kc, vc, nh, nkv, hd)
+        want = b.run(rows, pos)
+        reported = 0
+        for _ in range(20):
+            short.attention(a.q, a.kc, a.vc, bchip.F16, a.out, None, False, rows, nh, nkv, hd, pos,
+                            1.0 / math.sqrt(hd))
+            try:
+                short.sync()
+            except bchip.BchipError as e:
+                assert e.code == bchip.E_HIP and "timed out" in str(e)
+                reported += 1
+                got = short.read(a.out, (rows, nh, hd))
+                assert np.isnan(got).any()
+                continue
+            np.testing.assert_array_equal(short.read(a.out, (rows, nh, hd)), want)
+        print(f"{reported} of 20 calls ran out of their one poll", flush=True)
+        assert reported > 0
+        a.free()
+        b.free()
+    finally:
+        short.close()
+    # The other contexts are unaffected.
+    one, _ = ctxs
+    p = Pass(one, q, kc, vc, nh, nkv, hd)
+    np.testing.assert_array_equal(p.run(rows, pos), want)
+    p.free()
