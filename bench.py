@@ -97,17 +97,17 @@ def log(msg):
 class DecodeModel:
     """n_layer layers' caches and per-step inputs on the device, all generated there."""
 
-    def __init__(self, ctx, nh, nkv, hd, theta, neox, n_layer, ctx_len, steps, seed=1):
+    def __init__(self, ctx, nh, nkv, hd, theta, neox, n_layer, ctx_len, steps, seed=1, kv_type=bchip.F16):
         self.ctx, self.nh, self.nkv, self.hd, self.n_layer = ctx, nh, nkv, hd, n_layer
-        self.ctx_len, self.steps = ctx_len, steps
+        self.ctx_len, self.steps, self.kv_type = ctx_len, steps, kv_type
         kvd = nkv * hd
         cap = ctx_len + steps + 1
         self.kc, self.vc = [], []
         for layer in range(n_layer):
-            k = ctx.zeros(cap * kvd * 2)
-            v = ctx.zeros(cap * kvd * 2)
-            ctx.fill_normal(k, bchip.F16, ctx_len * kvd, seed * 1000 + 2 * layer)
-            ctx.fill_normal(v, bchip.F16, ctx_len * kvd, seed * 1000 + 2 * layer + 1)
+            k = ctx.zeros(cap * kvd * bchip.esize(kv_type))
+            v = ctx.zeros(cap * kvd * bchip.esize(kv_type))
+            ctx.fill_normal(k, kv_type, ctx_len * kvd, seed * 1000 + 2 * layer)
+            ctx.fill_normal(v, kv_type, ctx_len * kvd, seed * 1000 + 2 * layer + 1)
             self.kc.append(k)
             self.vc.append(v)
         # q, k, v of every (step, layer), positions of every step.
@@ -142,7 +142,7 @@ class DecodeModel:
             q, k, v = self.layer_ptrs(step, layer)
             if evs is not None and layer % every == 0:
                 ctx.timer_arm(evs[2 * (layer // every)], evs[2 * (layer // every) + 1])
-            ctx.rope_append_attention(q, k, v, self.kc[layer], self.vc[layer], bchip.F16, self.inv,
+            ctx.rope_append_attention(q, k, v, self.kc[layer], self.vc[layer], self.kv_type, self.inv,
                                       self.pos.ptr + 4 * step, self.nh, self.nkv, self.hd, self.hd, self.neox, slot,
                                       1.0 / math.sqrt(self.hd), self.out)
 
@@ -151,8 +151,9 @@ class DecodeModel:
             b.free()
 
 
-def bench_decode(ctx, hip, ctx_len, steps, warmup, n_layer=32, nh=32, nkv=8, hd=128, theta=5e5, neox=False):
-    m = DecodeModel(ctx, nh, nkv, hd, theta, neox, n_layer, ctx_len, steps + warmup)
+def bench_decode(ctx, hip, ctx_len, steps, warmup, n_layer=32, nh=32, nkv=8, hd=128, theta=5e5, neox=False,
+                 kv_type=bchip.F16):
+    m = DecodeModel(ctx, nh, nkv, hd, theta, neox, n_layer, ctx_len, steps + warmup, kv_type=kv_type)
     m.stream = ctx.stream()
     for s in range(warmup):
         m.step(s)
@@ -169,7 +170,7 @@ def bench_decode(ctx, hip, ctx_len, steps, warmup, n_layer=32, nh=32, nkv=8, hd=
     mean_kernel_ms = statistics.fmean(kernel_ms)
     # Visible slots grow by one per step: average algorithmic bytes over the timed launches.
     mean_len = ctx_len + warmup + (steps - 1) / 2 + 1
-    bytes_per_launch = 2 * mean_len * nkv * hd * 2
+    bytes_per_launch = 2 * mean_len * nkv * hd * bchip.esize(kv_type)
     gbs = bytes_per_launch / (mean_kernel_ms * 1e-3) / 1e9
     call_ms = total_ms / steps / n_layer  # one layer's whole call: decode kernel, fold, gaps
     return {
@@ -235,6 +236,57 @@ def bench_multirow(ctx, hip, rows, pos, nh, nkv, hd, reps, n_layer=1, verify=Fal
         res["hbm_frac"] = res["GBps"] / HBM_PEAK_GBS
         res["call_GBps"] = kv_bytes / (call_us * 1e-6) / 1e9
     return res
+
+
+def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=128, rows=8):
+    """configs[4]'s speculative decode as configured: 256 steps, each a pass of 8 draft rows
+    through the stage's 20 layers, every layer the reference's attention sub-sequence
+    (gpu/mod.rs:464-482) for 8 rows: bchip_rope_append (RoPE of q and k, the K/V append at the
+    rows' slots) then bchip_attention over the line; all drafts accepted, so the context grows
+    4096 -> 6136 by 8 a step. Timed as one region: the stream time of all 256 x 20 layer-steps."""
+    kvd = nkv * hd
+    cap = ctx0 + steps * rows
+    kcs, vcs = [], []
+    for layer in range(n_layer):
+        k, v = ctx.zeros(cap * kvd * 2), ctx.zeros(cap * kvd * 2)
+        ctx.fill_normal(k, bchip.F16, ctx0 * kvd, 700 + 2 * layer)
+        ctx.fill_normal(v, bchip.F16, ctx0 * kvd, 701 + 2 * layer)
+        kcs.append(k)
+        vcs.append(v)
+    per = rows * (nh + 2 * nkv) * hd  # a layer's q [rows][nh*hd], then k and v [rows][kvd]
+    qkv = ctx.zeros(n_layer * per * 4)
+    ctx.fill_normal(qkv, bchip.F32, n_layer * per, 699)
+    pos = ctx.upload(np.arange(ctx0, cap, dtype=np.uint32))
+    inv = ctx.upload(np.array([5e5 ** (-2.0 * i / hd) for i in range(hd // 2)], np.float32))
+    out = ctx.zeros(rows * nh * hd * 4)
+    scale = 1.0 / math.sqrt(hd)
+
+    def step(s):
+        base = ctx0 + s * rows
+        for layer in range(n_layer):
+            q = qkv.ptr + layer * per * 4
+            k = q + rows * nh * hd * 4
+            v = k + rows * kvd * 4
+            ctx.rope_append(q, k, v, kcs[layer], vcs[layer], bchip.F16, inv, pos.ptr + 4 * s * rows, rows, nh, nkv,
+                            hd, hd, False, base)
+            ctx.attention(q, kcs[layer], vcs[layer], bchip.F16, out, None, False, rows, nh, nkv, hd, base, scale)
+
+    step(0)  # warm (the step's appends are rewritten by the timed step 0)
+    ctx.sync()
+    ctx.timer_start()
+    for s in range(steps):
+        step(s)
+    total_ms = ctx.timer_stop()
+    for b in kcs + vcs + [qkv, pos, inv, out]:
+        b.free()
+    kv_bytes = sum(2.0 * (ctx0 + (s + 1) * rows) * kvd * 2 for s in range(steps)) * n_layer
+    layer_steps = steps * n_layer
+    return {"steps": steps, "rows": rows, "ctx": [ctx0, ctx0 + steps * rows], "layers": n_layer,
+            "calls_per_layer_step": "bchip_rope_append + bchip_attention", "total_ms": total_ms,
+            "us_per_layer_step": total_ms * 1e3 / layer_steps,
+            "tokens_per_s": rows * steps / (total_ms * 1e-3),
+            "kv_GBps": kv_bytes / (total_ms * 1e-3) / 1e9, "kv_hbm_frac": kv_bytes / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "note": "tokens_per_s: accepted draft tokens per second through the 20-layer stage's attention path"}
 
 
 def bench_ragged(ctx, hip, reps):
@@ -508,15 +560,15 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ctx", type=int, default=32768, help="visible slots of the headline decode")
-    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,ragged,calib,"
-                                               "products,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,f32,ragged,"
+                                               "calib,products,cpu")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build runs on one GPU; the attention path's "
                                    "split over several GPUs (by KV head or by sequence chunk) is a design, not run here"}))
         sys.exit(2)
-    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "ragged", "calib",
-                                                         "products", "cpu"}
+    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "f32", "ragged",
+                                                         "calib", "products", "cpu"}
     hip = Hip()
     extra = {}
     with bchip.Ctx(0) as ctx:
@@ -547,6 +599,22 @@ def main():
                 r = bench_multirow(ctx, hip, 8, ctx_len, 64, 8, 128, 10, n_layer=20, verify=True)
                 extra[f"verify_70b_{ctx_len}"] = r
                 log(json.dumps(r))
+            log("Llama-3-70B share: 256 verify steps of 8 rows, 20 layers, rope_append + attention a layer-step")
+            extra["verify_loop_70b_256"] = bench_verify_loop(ctx)
+            log(json.dumps(extra["verify_loop_70b_256"]))
+        if "f32" in want:
+            # The drop-in default: an unmodified binding passes the reference's f32 cache
+            # (bchip_rope_append_attention with BCHIP_F32: rope_append, then attn_f32).
+            log(f"f32-cache decode (the reference's cache type): configs[1] at {args.ctx} slots, configs[0]")
+            r = bench_decode(ctx, hip, args.ctx, 10, 2, kv_type=bchip.F32)
+            r["note"] = "f32 cache, f32 arithmetic (attn_f32): the path an unmodified binding runs"
+            extra[f"decode_f32_{args.ctx}"] = r
+            log(json.dumps(r))
+            r = bench_decode(ctx, hip, 512, args.steps, args.warmup, n_layer=24, nh=14, nkv=2, hd=64, theta=1e6,
+                             neox=True, kv_type=bchip.F32)
+            r["note"] = "configs[0]: Qwen2.5-0.5B-shaped, f32 cache at 512 slots, 24 layers; cache-resident"
+            extra["decode_qwen05b_512_f32"] = r
+            log(json.dumps(r))
         if "calib" in want:
             extra["copy_calibration"] = bench_copy_calibration(ctx, hip)
             log(json.dumps(extra["copy_calibration"]))

@@ -88,6 +88,9 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     };
     const uint32_t rlast = min(r0 + p.rb, p.rows) - 1u;
     const uint32_t maxlen = p.tree ? p.pos + ntail : p.pos + rlast + 1u;
+    // Slots at or past G * rb hold no query (a one-row step at G = 4 fills 4 of 16): the P v
+    // products, the folds and the stores skip them, whole iterations at a time (uniform).
+    const uint32_t used_e = min((uint32_t)F32_SLOTS, p.G * p.rb) * HD;
 
     for (uint32_t e = tid; e < F32_SLOTS * HD; e += F32_THREADS) {
         const uint32_t n = e / HD, d = e % HD;
@@ -166,6 +169,7 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
 #pragma unroll
             for (int i = 0; i < NP; i++) {
                 const uint32_t e = tid + F32_THREADS * i, n = e / HD, d = e % HD;
+                if (F32_THREADS * i >= used_e) break;
                 float acc = 0.0f;
                 for (int k = 0; k < F32_BLK; k++) acc += ps[n][k] * vs[k][d];
                 o[i] = o[i] * corr_s[n] + acc;
@@ -187,6 +191,7 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             const uint32_t n = (tid + F32_THREADS * i) / HD;
+            if (F32_THREADS * i >= used_e) break;
             R[i] = R[i] * fa[n] + o[i] * fb[n];
             o[i] = 0.0f;
         }
@@ -197,6 +202,7 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             const uint32_t e = tid + F32_THREADS * i, n = e / HD, d = e % HD;
+            if (F32_THREADS * i >= used_e) break;  // attn_combine reads no slot past them
             p.part_o[(u * F32_SLOTS + n) * HD + d] = o[i];
         }
         if (tid < (uint32_t)F32_SLOTS) *(float2*)(p.part_ml + (u * F32_SLOTS + tid) * 2) = float2{m, l};
