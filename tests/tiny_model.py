@@ -153,3 +153,64 @@ class RefModel:
 
     def logits(self, x) -> np.ndarray:
         return self._norm(np.asarray(x, np.float64), self.norm) @ self.out.T
+
+
+def wide_model_file(n_layer: int, neox: bool, seed: int = 7) -> bytes:
+    """A random model at the widths the measured kernels take (no reference counterpart; the
+    reference's fixture is the small one above): width 512, 4 query and 2 KV heads of head_dim
+    128, feed-forward 1024, vocabulary 256. The attention matrices and the head are Q8_0
+    (quantised from N(0, 1/width) draws by the oracle's quantiser), gate and up Q4K, down Q6K
+    (random blocks, their scales set so the weights stay modest), so every product of more
+    than one row runs on the matrix cores (widths a multiple of 256) and a one-row product on
+    the VALU. Weights from numpy's seeded generator, written by gguf.write_gguf."""
+    d, ff, vocab, heads, kv_heads = 512, 1024, 256, 4, 2
+    rng = np.random.default_rng(seed)
+    q8 = lambda rows, cols, s: O.quantize_q8_0(rng.standard_normal(rows * cols).astype(np.float32) * np.float32(s)).tobytes()
+    f32b = lambda v: np.asarray(v, "<f4").tobytes()
+
+    def kquant(wtype: int, rows: int, cols: int) -> bytes:
+        n, size = {12: (256, 144), 14: (256, 210)}[wtype]
+        data = rng.integers(0, 256, rows * cols // n * size, dtype=np.uint8).reshape(-1, size)
+        f16 = lambda x: np.frombuffer(np.float16(x).tobytes(), np.uint8)
+        if wtype == 12:  # Q4K: w = d sc q - dmin m, q in 0..15, sc and m in 0..63
+            data[:, 0:2] = f16(2.0 ** -12)
+            data[:, 2:4] = f16(7.5 * 2.0 ** -12)  # about centres the weights
+        else:  # Q6K: w = d sc (q - 32), sc an int8
+            data[:, 208:210] = f16(2.0 ** -14)
+        return data.tobytes()
+
+    kvd = d // heads * kv_heads
+    tensors = [("token_embd.weight", [d, vocab], 8, q8(vocab, d, 1.0))]
+    for l in range(n_layer):
+        p = lambda s: f"blk.{l}.{s}"
+        tensors += [
+            (p("attn_norm.weight"), [d], 0, f32b(rng.standard_normal(d).astype(np.float32) * 0.2 + 1.0)),
+            (p("attn_q.weight"), [d, d], 8, q8(d, d, d ** -0.5)),
+            (p("attn_k.weight"), [d, kvd], 8, q8(kvd, d, d ** -0.5)),
+            (p("attn_v.weight"), [d, kvd], 8, q8(kvd, d, d ** -0.5)),
+            (p("attn_q.bias"), [d], 0, f32b(rng.standard_normal(d).astype(np.float32) * 0.1)),
+            (p("attn_output.weight"), [d, d], 8, q8(d, d, d ** -0.5)),
+            (p("ffn_norm.weight"), [d], 0, f32b(rng.standard_normal(d).astype(np.float32) * 0.2 + 1.0)),
+            (p("ffn_gate.weight"), [d, ff], 12, kquant(12, ff, d)),
+            (p("ffn_up.weight"), [d, ff], 12, kquant(12, ff, d)),
+            (p("ffn_down.weight"), [ff, d], 14, kquant(14, d, ff)),
+        ]
+    tensors.append(("output_norm.weight", [d], 0, f32b(np.ones(d, np.float32))))
+    tensors.append(("output.weight", [d, vocab], 8, q8(vocab, d, d ** -0.5)))
+    arch = "qwen2" if neox else "llama"
+    tokens = ["<unk>", "<s>", "</s>"] + [f"t{i}" for i in range(vocab - 3)]
+    meta = [("general.architecture", "str", arch), ("general.name", "str", "wide"),
+            (f"{arch}.embedding_length", "u32", d), (f"{arch}.block_count", "u32", n_layer),
+            (f"{arch}.attention.head_count", "u32", heads), (f"{arch}.attention.head_count_kv", "u32", kv_heads),
+            (f"{arch}.feed_forward_length", "u32", ff), (f"{arch}.context_length", "u32", 4096),
+            (f"{arch}.rope.freq_base", "f32", 500000.0 if not neox else 1000000.0),
+            ("tokenizer.ggml.model", "str", "llama"), ("tokenizer.ggml.tokens", "strs", tokens),
+            ("tokenizer.ggml.scores", "f32s", [0.0] * vocab), ("tokenizer.ggml.bos_token_id", "u32", 1),
+            ("tokenizer.ggml.eos_token_id", "u32", 2)]
+    return write_gguf(meta, tensors)
+
+
+def wide_model(n_layer: int, neox: bool):
+    """wide_model_file loaded as a whole model, as tiny_model."""
+    cfg, layers, head, embd, _ = load_stage(wide_model_file(n_layer, neox), 0, n_layer, True, True)
+    return cfg, layers, head, embd
