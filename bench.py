@@ -560,15 +560,15 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--ctx", type=int, default=32768, help="visible slots of the headline decode")
-    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,f32,ragged,"
-                                               "calib,products,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: decode,short,prefill,verify,loop,f32,"
+                                               "ragged,calib,products,cpu")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build runs on one GPU; the attention path's "
                                    "split over several GPUs (by KV head or by sequence chunk) is a design, not run here"}))
         sys.exit(2)
-    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "f32", "ragged",
-                                                         "calib", "products", "cpu"}
+    want = set(args.only.split(",")) if args.only else {"decode", "short", "prefill", "verify", "loop", "f32",
+                                                         "ragged", "calib", "products", "cpu"}
     hip = Hip()
     extra = {}
     with bchip.Ctx(0) as ctx:
@@ -599,6 +599,7 @@ def main():
                 r = bench_multirow(ctx, hip, 8, ctx_len, 64, 8, 128, 10, n_layer=20, verify=True)
                 extra[f"verify_70b_{ctx_len}"] = r
                 log(json.dumps(r))
+        if "loop" in want:
             log("Llama-3-70B share: 256 verify steps of 8 rows, 20 layers, rope_append + attention a layer-step")
             extra["verify_loop_70b_256"] = bench_verify_loop(ctx)
             log(json.dumps(extra["verify_loop_70b_256"]))
