@@ -1306,6 +1306,168 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0xF70);
 }
 
+// Left fold of long chunk lists (more than CMB_RUN chunks: a long decode's or tree pass's
+// states, an f32 cache's split passes), one workgroup per (group, output slot). The slot's
+// chunk states go to LDS a segment at a time, every load of a segment in flight at once
+// (direct-to-LDS, 16 bytes a lane), where attn_combine's thread would wait for a round trip
+// every CMB_RUN chunks. Chunk c's weights come from the running maximum before it, which is
+// the prefix maximum of the chunk maxima (a max is exact in any order): a scan across the
+// threads, then merge_coef on the serial fold's operands. The threads of 4 dims each then run
+// the serial recurrence over the segment's chunks in order with attn_combine's expressions,
+// so the outputs are the same bits.
+constexpr int CMBL_THREADS = 256;
+constexpr int CMBL_BYTES = 112 * 1024;  // LDS of one segment's states
+
+template <int HD>
+__global__ __launch_bounds__(CMBL_THREADS) void attn_combine_long(const CombineParams p) {
+    constexpr uint32_t D4 = HD / 4;
+    constexpr uint32_t SEGC = CMBL_BYTES / (16 * D4) < CMBL_THREADS ? CMBL_BYTES / (16 * D4) : CMBL_THREADS;  // chunks a segment
+    constexpr uint32_t NLD = SEGC * D4 / CMBL_THREADS;          // loads a thread a segment
+    static_assert(SEGC % 8 == 0, "the recurrence reads eight chunks a batch, 16-byte aligned");
+    static_assert(NLD * CMBL_THREADS == SEGC * D4 && SEGC <= CMBL_THREADS, "a segment's loads and chunks fit the threads");
+    __shared__ __attribute__((aligned(16))) float4 so[SEGC * D4];
+    __shared__ __attribute__((aligned(16))) float cw[3][SEGC];  // per chunk: a, b and its sum l
+    __shared__ float mls[2][CMBL_THREADS];  // the segment's chunk maxima and sums
+    const uint32_t hd = p.hd, slots_out = p.slots_out, ngroups = p.ngroups, shared = p.shared, nrb = p.nrb,
+                   rb = p.rb, G = p.G, rows = p.rows, nch_s = p.nchunk, nkv = p.nkv;
+    const uint32_t grp = blockIdx.x / slots_out, slot = blockIdx.x % slots_out;
+    if (grp >= ngroups) return;
+    uint32_t unit0, nchunk, r, h, step;  // chunk c's state is unit unit0 + c * step
+    if (shared) {
+        const uint32_t kvh = grp / nrb, rbi = grp % nrb;
+        const uint32_t gh = slot / rb, rl = slot % rb;
+        r = rbi * rb + rl;
+        if (gh >= G || r >= rows) return;
+        h = kvh * G + gh;
+        unit0 = grp * nch_s;
+        nchunk = nch_s;
+        step = 1;
+    } else {  // decode kernel states, in (item, chunk, KV head) order
+        const uint32_t item = grp / nkv, kvh = grp % nkv;
+        const Item& I = p.items[item];
+        if (slot / G >= I.nrows || I.nchunk == 1) return;  // one chunk: written directly
+        r = I.row + slot / G;
+        h = kvh * G + slot % G;
+        unit0 = I.unit0 + kvh;
+        nchunk = I.nchunk;
+        step = nkv;
+    }
+    // The state index of chunk c (unit unit0 + c * step, slot `slot`) fits 32 bits: the
+    // workspace could not hold 2^32 states.
+    const uint32_t stride = p.slots;  // partial slots per unit
+    auto state = [&](uint32_t c) { return (unit0 + c * step) * stride + slot; };
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    typedef __attribute__((address_space(3))) void lds_t;
+    // Barriers without a fence: the waits before them are explicit (a fence would wait for
+    // every direct-to-LDS load in flight, the states' included).
+    auto barrier = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    float M = -INFINITY;  // wave 0: the running max before the segment
+    float L = 0.0f, O = 0.0f;  // threads tid < HD: the fold of dim tid and of the sums
+    for (uint32_t c0 = 0; c0 < nchunk; c0 += SEGC) {
+        const uint32_t nseg = min(SEGC, nchunk - c0);
+        barrier();  // wave 0 is done with the previous segment's LDS
+        // Chunk c0 + 64 wave + lane's max and sum (two 4-byte loads), then the states: load i
+        // of the workgroup, lane l, fills so[256 i + 64 wave + l] with 16 bytes of chunk
+        // c0 + e / D4 (e that index). Chunks past the list load its last.
+        {
+            const float* src = p.part_ml + (size_t)state(min(c0 + 64 * wave + lane, nchunk - 1u)) * 2;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_t*)&mls[0][64 * wave], 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(src + 1), (lds_t*)&mls[1][64 * wave], 4, 0, 0);
+        }
+        // (Load i's chunk is c0 + i * CPL + tid / D4, its dims 4 (tid % D4) .. + 3.)
+        constexpr uint32_t CPL = CMBL_THREADS / D4;  // chunks a workgroup load covers
+        static_assert(CMBL_THREADS % D4 == 0, "a load covers whole chunks");
+        const float* ob = p.part_o + 4 * (tid % D4);
+#pragma unroll
+        for (uint32_t i = 0; i < NLD; i++) {
+            const uint32_t c = min(c0 + i * CPL + tid / D4, nchunk - 1u);
+            __builtin_amdgcn_global_load_lds((const void*)(ob + (size_t)state(c) * HD),
+                                             (lds_t*)&so[i * CMBL_THREADS + 64 * wave], 16, 0, 0);
+        }
+        wait_vm<NLD>();  // this wave's maxima and sums are in
+        barrier();       // and every wave's
+        if (wave == 0) {
+            // Lane l's four chunks 4l .. 4l + 3: their maxima (-inf past the segment), the
+            // prefix within the four, then the wave's exclusive scan of the lanes' maxima.
+            float mv[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) mv[j] = 4 * lane + j < nseg ? mls[0][4 * lane + j] : -INFINITY;
+            const float tot = fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3]));
+            float inc = tot;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const float t = __shfl_up(inc, d);
+                if (lane >= (uint32_t)d) inc = fmaxf(inc, t);
+            }
+            float run = __shfl_up(inc, 1);
+            run = lane == 0 ? M : fmaxf(M, run);  // the running max before chunk 4l
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t c = 4 * lane + j;
+                float a, b, mn;
+                merge_coef(run, mv[j], a, b, mn);
+                if (c < nseg) {
+                    cw[0][c] = a;
+                    cw[1][c] = b;
+                    cw[2][c] = mls[1][c];
+                }
+                run = mn;
+            }
+            M = fmaxf(M, __shfl(inc, 63));
+        }
+        wait_vm<0>();
+        barrier();  // every wave's states are in
+        if (tid < HD) {
+            // Thread d: dim d's recurrence (and the sum's, the same in every thread). Full
+            // batches of eight chunks as straight-line code, their reads issued first; then
+            // the segment's last chunks one at a time.
+            const float* sof = (const float*)so;
+            auto step = [&](float a, float b, float l, float o) {
+                L = L * a + l * b;
+                O = O * a + o * b;
+            };
+            // A batch: its eight chunks' a, b and l as 16-byte broadcast reads, and dim d of
+            // their states. The next batch's reads go out before this batch's steps
+            // (unconditionally: past the segment they read entries no step uses).
+            struct Batch {
+                float4 a[2], b[2], l[2];
+                float o[8];
+            };
+            auto read = [&](uint32_t c, Batch& B) {
+#pragma unroll
+                for (uint32_t k = 0; k < 2; k++) {
+                    B.a[k] = *(const float4*)&cw[0][c + 4 * k];
+                    B.b[k] = *(const float4*)&cw[1][c + 4 * k];
+                    B.l[k] = *(const float4*)&cw[2][c + 4 * k];
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 8; j++) B.o[j] = sof[(c + j) * HD + tid];
+            };
+            Batch cur;
+            read(0, cur);
+            uint32_t c = 0;
+            for (; c + 8 <= nseg; c += 8) {
+                Batch nxt;
+                read(c + 8 < SEGC ? c + 8 : 0u, nxt);
+#pragma unroll
+                for (uint32_t k = 0; k < 2; k++) {
+                    step(cur.a[k].x, cur.b[k].x, cur.l[k].x, cur.o[4 * k]);
+                    step(cur.a[k].y, cur.b[k].y, cur.l[k].y, cur.o[4 * k + 1]);
+                    step(cur.a[k].z, cur.b[k].z, cur.l[k].z, cur.o[4 * k + 2]);
+                    step(cur.a[k].w, cur.b[k].w, cur.l[k].w, cur.o[4 * k + 3]);
+                }
+                cur = nxt;
+            }
+            for (; c < nseg; c++) step(cw[0][c], cw[1][c], cw[2][c], sof[c * HD + tid]);
+        }
+    }
+    if (tid < hd) p.out[((size_t)r * p.nh + h) * hd + tid] = O / L;
+}
+
 // V^T tiles of a prefill call (written by vt_pack): per KV head, hd rows of npad keys, each
 // 32-key group stored in the order the PV operand takes it (lane group g holds keys
 // 4g..4g+3 and 16+4g..16+4g+3), so that a lane's eight keys of one dim are 16 contiguous
@@ -2201,6 +2363,14 @@ static uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1)
 template <int HD>
 static hipError_t launch_combine_t(CombineParams& cp, uint32_t groups, hipStream_t s) {
     cp.ngroups = groups;
+    // Lists of more than CMB_RUN chunks: the long fold, a workgroup per output slot.
+    uint32_t most = cp.shared ? cp.nchunk : 0u;
+    if (!cp.shared)
+        for (uint32_t i = 0; i < cp.nitems; i++) most = std::max(most, cp.items[i].nchunk);
+    if (cp.long_fold && most > (uint32_t)CMB_RUN) {
+        hipLaunchKernelGGL((attn_combine_long<HD>), dim3((uint64_t)groups * cp.slots_out), dim3(CMBL_THREADS), 0, s, cp);
+        return hipGetLastError();
+    }
     const uint64_t threads = (uint64_t)groups * cp.slots_out * (cp.hd / 4);
     const dim3 grid(ceil_div(threads, CMB_THREADS)), block(CMB_THREADS);
     const uint32_t nc = cp.shared ? cp.nchunk : (uint32_t)CMB_RUN;
@@ -2405,6 +2575,7 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
     dp.part_o = ws.o;
     dp.part_ml = ws.ml;
     CombineParams cp{};
+    cp.long_fold = ws.combine_long;
     cp.zero = ws.zero;
     cp.out = a.out;
     cp.part_o = ws.o;
@@ -2513,6 +2684,7 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     }
     if (e != hipSuccess || !sp.split || gfold) return e;
     CombineParams cp{};
+    cp.long_fold = ws.combine_long;
     cp.zero = ws.zero;
     cp.out = a.out;
     cp.part_o = ws.o;

@@ -281,6 +281,7 @@ hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipSt
     }
     if (e != hipSuccess || !fp.split) return e;
     CombineParams cp{};
+    cp.long_fold = ws.combine_long;
     cp.zero = ws.zero;
     cp.out = a.out;
     cp.part_o = ws.o;

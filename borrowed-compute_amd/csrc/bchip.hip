@@ -185,6 +185,7 @@ void Workspace::set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_
     group_fold = owner.group_fold;
     group_spread = owner.group_spread;
     group_spins = owner.group_spins;
+    combine_long = owner.combine_long;
     gerr = owner.gerr;
     gerr_host = owner.gerr_host;
 }
@@ -253,6 +254,8 @@ hipError_t Workspace::init(int device) {
     const char* gf = getenv("BCHIP_GROUP_FOLD");
     group_fold = !(gf && strcmp(gf, "0") == 0);
     group_spread = gf && strcmp(gf, "spread") == 0;
+    const char* cl = getenv("BCHIP_COMBINE_LONG");
+    combine_long = !(cl && strcmp(cl, "0") == 0);
     if (const char* sp = getenv("BCHIP_GROUP_FOLD_SPINS")) {
         const long v = strtol(sp, nullptr, 10);
         if (v > 0 && v < (1l << 24)) group_spins = (uint32_t)v;

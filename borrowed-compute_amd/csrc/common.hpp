@@ -180,6 +180,7 @@ struct CombineParams {
     uint32_t rows, rb, nrb, nchunk; // shared launches
     uint32_t ngroups;  // groups in the launch
     uint32_t nitems;
+    uint32_t long_fold;  // host: lists of more than CMB_RUN chunks may take attn_combine_long
     Item items[MAX_ITEMS];
 };
 

@@ -28,6 +28,9 @@ struct Workspace {
     bool group_fold = true;
     uint32_t group_spread = 0;
     uint32_t group_spins = 1u << 16;
+    // BCHIP_COMBINE_LONG=0 at init: lists of more than CMB_RUN chunks fold in attn_combine
+    // as shorter ones do, not in attn_combine_long (the same bits; for tests).
+    bool combine_long = true;
     uint32_t* gerr = nullptr;       // device address of the host word
     volatile uint32_t* gerr_host = nullptr;
     void* vt = nullptr;    // V^T tiles of a prefill call; the sampler's keys and sort scratch
