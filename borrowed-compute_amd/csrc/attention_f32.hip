@@ -47,17 +47,26 @@ struct F32Params {
     uint32_t rb, nrb; // rows a workgroup (1 for trees), row blocks
     uint32_t nchunk;  // chunks of the farthest list
     uint32_t split;   // a workgroup per chunk
+    const float* zero;  // ZERO_BYTES of zeros: the loads of rows past a list
 };
 
 template <int HD>
 __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
-    constexpr int QS = HD + 1;                         // LDS row stride of q and K: rows on distinct banks
     constexpr int NP = F32_SLOTS * HD / F32_THREADS;  // (slot, dim) outputs a thread
     static_assert(NP >= 1 && (F32_SLOTS * HD) % F32_THREADS == 0, "outputs divide over the threads");
-    __shared__ float qs[F32_SLOTS][QS];
-    __shared__ float ks[F32_BLK][QS];
+    // q and K rows in LDS in lane order: element d = j + 8i at j * JS + i, so that score lane
+    // j's elements (d = j, j + 8, ...) are contiguous and read 16 bytes at a time; JS pads a
+    // lane's run so that the eight lanes of an entry read eight distinct groups of banks.
+    constexpr int NI = HD / 8;                    // elements a score lane takes
+    constexpr int JS = NI % 8 == 0 ? NI + 4 : NI;  // LDS stride between lanes' runs
+    constexpr int KS = 8 * JS;                    // LDS row of q or K
+    static_assert(NI % 4 == 0, "a lane's run is whole 16-byte reads");
+    constexpr int NL = F32_BLK * (HD / 4) / F32_THREADS;  // 16-byte pieces of K (and of V) a thread loads a block
+    static_assert(NL >= 1 && F32_BLK * (HD / 4) % F32_THREADS == 0, "a block's rows divide over the threads");
+    __shared__ __attribute__((aligned(16))) float qs[F32_SLOTS][KS];
+    __shared__ __attribute__((aligned(16))) float ks[F32_BLK][KS];
     __shared__ __attribute__((aligned(16))) float vs[F32_BLK][HD];
-    __shared__ float ps[F32_SLOTS][F32_BLK + 1];
+    __shared__ __attribute__((aligned(16))) float ps[F32_SLOTS][F32_BLK + 4];  // rows 16-byte aligned
     __shared__ float corr_s[F32_SLOTS], fa[F32_SLOTS], fb[F32_SLOTS], lsum[F32_SLOTS];
     __shared__ uint32_t tail[MAX_ITEMS];
 
@@ -99,70 +108,148 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
             v = p.q[((size_t)r * p.nh + h) * hd + d];
         }
-        qs[n][d] = v;
+        qs[n][(d % 8) * JS + d / 8] = v;
     }
 
     float o[NP], R[NP];
 #pragma unroll
     for (int i = 0; i < NP; i++) o[i] = R[i] = 0.0f;
-    float m = -INFINITY, l = 0.0f, RM = -INFINITY, RL = 0.0f;  // slot threads (tid < F32_SLOTS)
+    // Slot n's running state: m in lanes 4n .. 4n + 3 of wave 0 (the softmax's lanes of the
+    // slot), l, RM and RL in lane 4n.
+    float m = -INFINITY, l = 0.0f, RM = -INFINITY, RL = 0.0f;
+    const bool slot_lane = tid < 4u * F32_SLOTS && (tid & 3u) == 0u;
+    const uint32_t sn = tid >> 2;  // the slot of a softmax lane
+
+    // This thread's share of a block's K and V rows (NL 16-byte pieces of each), loaded one
+    // block ahead: the next block's loads are in flight while this block computes. Entries
+    // past the chunk or the cache, and dims past hd, load the zero page.
+    f32x4 kr[NL], vr[NL];
+    auto fetch = [&](uint32_t key0, uint32_t kb1) {
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const uint32_t e = tid + F32_THREADS * i, k = e / (HD / 4), d = 4 * (e % (HD / 4)), kk = key0 + k;
+            const uint32_t s = (p.tree && kk >= p.pos) ? tail[min(kk - p.pos, (uint32_t)MAX_ITEMS - 1u)] : kk;
+            const bool ok = kk < kb1 && d < hd && (uint64_t)s < p.slot_limit;
+            // One load each from a selected address (the asm keeps the compiler from
+            // splitting it into a load on each side of a branch, each followed by a wait).
+            uintptr_t ka = ok ? (uintptr_t)(kcb + (size_t)s * kvd + d) : (uintptr_t)p.zero;
+            uintptr_t va = ok ? (uintptr_t)(vcb + (size_t)s * kvd + d) : (uintptr_t)p.zero;
+            asm("" : "+v"(ka), "+v"(va));
+            typedef __attribute__((address_space(1))) const f32x4 gf4;
+            kr[i] = *(gf4*)ka;
+            vr[i] = *(gf4*)va;
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const uint32_t e = tid + F32_THREADS * i, k = e / (HD / 4), d = 4 * (e % (HD / 4));
+            float* kd = &ks[k][(d % 8) * JS + d / 8];  // d % 8 is 0 or 4: elements d .. d + 3 are lanes' runs apart
+            kd[0] = kr[i][0];
+            kd[JS] = kr[i][1];
+            kd[2 * JS] = kr[i][2];
+            kd[3 * JS] = kr[i][3];
+            *(f32x4*)&vs[k][d] = vr[i];
+        }
+    };
+    // Scores: slot by slot, thread (entry qk, lane qj) sums q[d] k[d] over d = qj, qj + 8, ...
+    // in order (quant::dot's lane qj), and lane 0 of each eight adds the eight sums to 0 in
+    // lane order (row shifts within the 16-lane row).
+    const uint32_t qk = tid >> 3, qj = tid & 7;
+    const uint32_t nused = used_e / HD;  // slots that may hold a query
 
     const uint32_t cend = p.split ? c_one + 1u : max(1u, (maxlen + CHUNK_MULTI - 1u) / CHUNK_MULTI);
     for (uint32_t c = c_one; c < cend; c++) {
         const uint32_t kb0 = c * CHUNK_MULTI, kb1 = min(kb0 + CHUNK_MULTI, maxlen);
+        if (kb0 < kb1) fetch(kb0, kb1);
         for (uint32_t key0 = kb0; key0 < kb1; key0 += F32_BLK) {
             __syncthreads();  // the previous block's K, V and P are consumed (and q is in)
-            for (uint32_t e = tid; e < F32_BLK * (HD / 4); e += F32_THREADS) {
-                const uint32_t k = e / (HD / 4), d = 4 * (e % (HD / 4)), kk = key0 + k;
-                float4 kv = float4{0.0f, 0.0f, 0.0f, 0.0f}, vv = kv;
-                if (kk < kb1 && d < hd) {
-                    const uint32_t s = (p.tree && kk >= p.pos) ? tail[kk - p.pos] : kk;
-                    if ((uint64_t)s < p.slot_limit) {
-                        kv = *(const float4*)(kcb + (size_t)s * kvd + d);
-                        vv = *(const float4*)(vcb + (size_t)s * kvd + d);
-                    }
-                }
-                ks[k][d] = kv.x;
-                ks[k][d + 1] = kv.y;
-                ks[k][d + 2] = kv.z;
-                ks[k][d + 3] = kv.w;
-                *(float4*)&vs[k][d] = vv;
-            }
-            __syncthreads();
+            stash();
+            if (key0 + F32_BLK < kb1) fetch(key0 + F32_BLK, kb1);
+            // K and V in for everyone. The fences order LDS only: __syncthreads' would also
+            // wait for the next block's loads just issued.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             // Scores of (slot, entry) pairs: quant::dot's eight lane sums, then times sc;
             // entries at or past a slot's list are -inf.
-            for (uint32_t e = tid; e < F32_SLOTS * F32_BLK; e += F32_THREADS) {
-                const uint32_t n = e / F32_BLK, k = e % F32_BLK;
-                float s = -INFINITY;
-                if (key0 + k < slot_len(n)) {
-                    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-                    for (uint32_t d = 0; d < hd; d += 8) {
+            // Two slots at a time (each K value read once for both; a slot past nused computes
+            // on zeros and is not written); the lane's steps unrolled over HD, so its LDS reads
+            // go out ahead of the sums that take them.
+            auto lane_sum = [&](float acc) {  // lane 0 of each eight: 0 + acc_0 + ... + acc_7
+                const int ai = __float_as_int(acc);
+                float dsum = 0.0f + acc;
+                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x101, 0xf, 0xf, false));
+                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x102, 0xf, 0xf, false));
+                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x103, 0xf, 0xf, false));
+                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x104, 0xf, 0xf, false));
+                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x105, 0xf, 0xf, false));
+                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x106, 0xf, 0xf, false));
+                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x107, 0xf, 0xf, false));
+                return dsum;
+            };
+            for (uint32_t n = 0; n < nused; n += 2) {
+                float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
-                        for (int j = 0; j < 8; j++) acc[j] += qs[n][d + j] * ks[k][d + j];
+                for (uint32_t i = 0; i < (uint32_t)NI; i += 4) {
+                    const f32x4 kv = *(const f32x4*)&ks[qk][qj * JS + i];
+                    const f32x4 q0 = *(const f32x4*)&qs[n][qj * JS + i];
+                    const f32x4 q1 = *(const f32x4*)&qs[n + 1][qj * JS + i];
+#pragma unroll
+                    for (uint32_t t = 0; t < 4; t++) {
+                        if (8 * (i + t) < hd) {  // d = qj + 8 (i + t) in order; past hd nothing
+                            acc0 += q0[t] * kv[t];
+                            acc1 += q1[t] * kv[t];
+                        }
                     }
-                    float dsum = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) dsum += acc[j];
-                    s = dsum * p.sc;
                 }
-                ps[n][k] = s;
+                const float s0 = lane_sum(acc0), s1 = lane_sum(acc1);
+                if (qj == 0) {
+                    ps[n][qk] = (key0 + qk < slot_len(n)) ? s0 * p.sc : -INFINITY;
+                    if (n + 1 < nused) ps[n + 1][qk] = (key0 + qk < slot_len(n + 1)) ? s1 * p.sc : -INFINITY;
+                }
             }
+            for (uint32_t e = nused * F32_BLK + tid; e < F32_SLOTS * F32_BLK; e += F32_THREADS)
+                ps[e / F32_BLK][e % F32_BLK] = -INFINITY;
             __syncthreads();
             // Per slot: the block's max, the new running max, P and the block's sum of P.
-            if (tid < (uint32_t)F32_SLOTS) {
-                float mx = -INFINITY;
-                for (int k = 0; k < F32_BLK; k++) mx = fmaxf(mx, ps[tid][k]);
+            // Lanes 4n .. 4n + 3 of wave 0 take slot n's entries eight each: the block's max
+            // across the four (a max is exact in any order), P in parallel, and the block's
+            // sum in entry order by lane 4n (its own eight, then the others' from LDS).
+            static_assert(F32_BLK == 32 && 4 * F32_SLOTS == 64, "wave 0 holds every slot's softmax");
+            if (tid < 4u * F32_SLOTS) {
+                const uint32_t k0 = 8 * (tid & 3u);
+                f32x4 pa = *(const f32x4*)&ps[sn][k0], pb = *(const f32x4*)&ps[sn][k0 + 4];
+                float mx = fmaxf(fmaxf(fmaxf(pa[0], pa[1]), fmaxf(pa[2], pa[3])), fmaxf(fmaxf(pb[0], pb[1]), fmaxf(pb[2], pb[3])));
+                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0xB1, 0xf, 0xf, false)));
+                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x4E, 0xf, 0xf, false)));
                 const float mn = fmaxf(m, mx), ms = (mn == -INFINITY) ? 0.0f : mn;
                 const float cr = exp2_hw(m - ms);
-                float bl = 0.0f;
-                for (int k = 0; k < F32_BLK; k++) {
-                    const float pe = exp2_hw(ps[tid][k] - ms);
-                    ps[tid][k] = pe;
-                    bl += pe;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    pa[t] = exp2_hw(pa[t] - ms);
+                    pb[t] = exp2_hw(pb[t] - ms);
                 }
-                l = l * cr + bl;
+                *(f32x4*)&ps[sn][k0] = pa;
+                *(f32x4*)&ps[sn][k0 + 4] = pb;
+                if ((tid & 3u) == 0u) {
+                    float bl = 0.0f;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) bl += pa[t];
+#pragma unroll
+                    for (int t = 0; t < 4; t++) bl += pb[t];
+#pragma unroll
+                    for (int k = 8; k < F32_BLK; k += 4) {
+                        const f32x4 c = *(const f32x4*)&ps[sn][k];
+                        bl += c[0];
+                        bl += c[1];
+                        bl += c[2];
+                        bl += c[3];
+                    }
+                    l = l * cr + bl;
+                    corr_s[sn] = cr;
+                }
                 m = mn;
-                corr_s[tid] = cr;
             }
             __syncthreads();
             // O = O * corr + sum of P v, the sum in entry order.
@@ -177,16 +264,16 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
         }
         if (p.split) break;
         // The chunk's state folded into the running one (merge_coef, R = R a + c b).
-        if (tid < (uint32_t)F32_SLOTS) {
+        if (slot_lane) {
             float a, b, mn;
             merge_coef(RM, m, a, b, mn);
             RL = RL * a + l * b;
             RM = mn;
-            fa[tid] = a;
-            fb[tid] = b;
-            m = -INFINITY;
-            l = 0.0f;
+            fa[sn] = a;
+            fb[sn] = b;
         }
+        m = -INFINITY;
+        l = 0.0f;
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < NP; i++) {
@@ -205,10 +292,10 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             if (F32_THREADS * i >= used_e) break;  // attn_combine reads no slot past them
             p.part_o[(u * F32_SLOTS + n) * HD + d] = o[i];
         }
-        if (tid < (uint32_t)F32_SLOTS) *(float2*)(p.part_ml + (u * F32_SLOTS + tid) * 2) = float2{m, l};
+        if (slot_lane) *(float2*)(p.part_ml + (u * F32_SLOTS + sn) * 2) = float2{m, l};
         return;
     }
-    if (tid < (uint32_t)F32_SLOTS) lsum[tid] = RL;
+    if (slot_lane) lsum[sn] = RL;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NP; i++) {
@@ -248,6 +335,7 @@ hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipSt
     if (fp.G > (uint32_t)F32_SLOTS) return hipErrorInvalidValue;
     fp.pos = a.pos;
     fp.slot_limit = a.slot_limit > kvoff ? a.slot_limit - kvoff : 0;
+    fp.zero = (const float*)ws.zero;
     fp.sc = a.scale * LOG2E;
     fp.rb = a.tree ? 1u : std::max<uint32_t>(1u, (uint32_t)F32_SLOTS / fp.G);
     if (fp.rb > a.rows) fp.rb = a.rows;
