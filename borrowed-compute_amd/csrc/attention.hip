@@ -1381,12 +1381,17 @@ __global__ __launch_bounds__(CMBL_THREADS) void attn_combine_long(const CombineP
         // (Load i's chunk is c0 + i * CPL + tid / D4, its dims 4 (tid % D4) .. + 3.)
         constexpr uint32_t CPL = CMBL_THREADS / D4;  // chunks a workgroup load covers
         static_assert(CMBL_THREADS % D4 == 0, "a load covers whole chunks");
+        // Load i's address: the first load's plus i steps of CPL chunks (chunk states are
+        // step * stride apart), or the list's last chunk's once past it.
         const float* ob = p.part_o + 4 * (tid % D4);
+        const uint32_t cf = c0 + tid / D4;
+        const float* a0 = ob + (size_t)state(min(cf, nchunk - 1u)) * HD;
+        const float* alast = ob + (size_t)state(nchunk - 1u) * HD;
+        const size_t inc = (size_t)CPL * step * stride * HD;
 #pragma unroll
         for (uint32_t i = 0; i < NLD; i++) {
-            const uint32_t c = min(c0 + i * CPL + tid / D4, nchunk - 1u);
-            __builtin_amdgcn_global_load_lds((const void*)(ob + (size_t)state(c) * HD),
-                                             (lds_t*)&so[i * CMBL_THREADS + 64 * wave], 16, 0, 0);
+            const float* src = cf + i * CPL < nchunk ? a0 + i * inc : alast;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_t*)&so[i * CMBL_THREADS + 64 * wave], 16, 0, 0);
         }
         wait_vm<NLD>();  // this wave's maxima and sums are in
         barrier();       // and every wave's
@@ -1421,49 +1426,35 @@ __global__ __launch_bounds__(CMBL_THREADS) void attn_combine_long(const CombineP
         }
         wait_vm<0>();
         barrier();  // every wave's states are in
-        if (tid < HD) {
-            // Thread d: dim d's recurrence (and the sum's, the same in every thread). Full
-            // batches of eight chunks as straight-line code, their reads issued first; then
-            // the segment's last chunks one at a time.
-            const float* sof = (const float*)so;
-            auto step = [&](float a, float b, float l, float o) {
-                L = L * a + l * b;
-                O = O * a + o * b;
-            };
-            // A batch: its eight chunks' a, b and l as 16-byte broadcast reads, and dim d of
-            // their states. The next batch's reads go out before this batch's steps
-            // (unconditionally: past the segment they read entries no step uses).
-            struct Batch {
-                float4 a[2], b[2], l[2];
-                float o[8];
-            };
-            auto read = [&](uint32_t c, Batch& B) {
+        // Thread d < HD: dim d's recurrence. The sums' recurrence runs in the wave after the
+        // dims' (every dims thread runs it as well when the dims take all four waves). Full
+        // runs of 32 chunks are straight-line code, so the compiler issues their LDS reads
+        // ahead of the steps that take them; then runs of 8, then single chunks.
+        const float* sof = (const float*)so;
+        constexpr bool SPARE = HD < CMBL_THREADS;  // a wave past the dims computes the sums
+        const bool dims = tid < (uint32_t)HD, sums = SPARE ? (tid >= (uint32_t)HD && tid < (uint32_t)HD + 64u) : dims;
+        auto run = [&](uint32_t c, auto N) {
+            constexpr uint32_t n = decltype(N)::value;
+            if (dims) {
 #pragma unroll
-                for (uint32_t k = 0; k < 2; k++) {
-                    B.a[k] = *(const float4*)&cw[0][c + 4 * k];
-                    B.b[k] = *(const float4*)&cw[1][c + 4 * k];
-                    B.l[k] = *(const float4*)&cw[2][c + 4 * k];
-                }
-#pragma unroll
-                for (uint32_t j = 0; j < 8; j++) B.o[j] = sof[(c + j) * HD + tid];
-            };
-            Batch cur;
-            read(0, cur);
-            uint32_t c = 0;
-            for (; c + 8 <= nseg; c += 8) {
-                Batch nxt;
-                read(c + 8 < SEGC ? c + 8 : 0u, nxt);
-#pragma unroll
-                for (uint32_t k = 0; k < 2; k++) {
-                    step(cur.a[k].x, cur.b[k].x, cur.l[k].x, cur.o[4 * k]);
-                    step(cur.a[k].y, cur.b[k].y, cur.l[k].y, cur.o[4 * k + 1]);
-                    step(cur.a[k].z, cur.b[k].z, cur.l[k].z, cur.o[4 * k + 2]);
-                    step(cur.a[k].w, cur.b[k].w, cur.l[k].w, cur.o[4 * k + 3]);
-                }
-                cur = nxt;
+                for (uint32_t j = 0; j < n; j++) O = O * cw[0][c + j] + sof[(c + j) * HD + tid] * cw[1][c + j];
             }
-            for (; c < nseg; c++) step(cw[0][c], cw[1][c], cw[2][c], sof[c * HD + tid]);
-        }
+            if (sums) {
+#pragma unroll
+                for (uint32_t j = 0; j < n; j++) L = L * cw[0][c + j] + cw[2][c + j] * cw[1][c + j];
+            }
+        };
+        uint32_t c = 0;
+        for (; c + 32 <= nseg; c += 32) run(c, std::integral_constant<uint32_t, 32>{});
+        for (; c + 8 <= nseg; c += 8) run(c, std::integral_constant<uint32_t, 8>{});
+        for (; c < nseg; c++) run(c, std::integral_constant<uint32_t, 1>{});
+    }
+    // The sums' lane hands L to the dims.
+    __shared__ float lfin;
+    if constexpr (HD < CMBL_THREADS) {
+        if (tid == (uint32_t)HD) lfin = L;
+        __syncthreads();
+        L = lfin;
     }
     if (tid < hd) p.out[((size_t)r * p.nh + h) * hd + tid] = O / L;
 }
