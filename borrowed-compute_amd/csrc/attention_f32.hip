@@ -52,22 +52,24 @@ struct F32Params {
 
 template <int HD>
 __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
-    constexpr int NP = F32_SLOTS * HD / F32_THREADS;  // (slot, dim) outputs a thread
-    static_assert(NP >= 1 && (F32_SLOTS * HD) % F32_THREADS == 0, "outputs divide over the threads");
-    // q and K rows in LDS in lane order: element d = j + 8i at j * JS + i, so that score lane
-    // j's elements (d = j, j + 8, ...) are contiguous and read 16 bytes at a time; JS pads a
-    // lane's run so that the eight lanes of an entry read eight distinct groups of banks.
-    constexpr int NI = HD / 8;                    // elements a score lane takes
-    constexpr int JS = NI % 8 == 0 ? NI + 4 : NI;  // LDS stride between lanes' runs
-    constexpr int KS = 8 * JS;                    // LDS row of q or K
+    // q and K rows in LDS in lane order: element d = j + 8i at j * NI + i, so that the
+    // elements of quant::dot's lane j (d = j, j + 8, ...) are contiguous and read 16 bytes at a
+    // time. Rows are KS floats apart, 4 more than a multiple of 32 banks, so that the eight
+    // lanes LDS serves together (eight entries, one offset) hit eight groups of banks.
+    constexpr int NI = HD / 8;     // elements of one dot lane
+    constexpr int KS = HD + 4;     // LDS row of q or K
     static_assert(NI % 4 == 0, "a lane's run is whole 16-byte reads");
     constexpr int NL = F32_BLK * (HD / 4) / F32_THREADS;  // 16-byte pieces of K (and of V) a thread loads a block
     static_assert(NL >= 1 && F32_BLK * (HD / 4) % F32_THREADS == 0, "a block's rows divide over the threads");
+    // Each wave takes slots wave, wave + W, ...: their scores, softmax and P v within the wave.
+    constexpr int W = F32_THREADS / 64;            // waves
+    constexpr int SPW = F32_SLOTS / W;             // slots a wave at most
+    constexpr int DPL = HD >= 64 ? HD / 64 : 1;    // dims a lane holds in P v
+    constexpr int DL = HD / DPL;                   // lanes holding dims
+    static_assert(F32_BLK == 32, "a block's entries are the wave's lanes 0..31");
     __shared__ __attribute__((aligned(16))) float qs[F32_SLOTS][KS];
     __shared__ __attribute__((aligned(16))) float ks[F32_BLK][KS];
     __shared__ __attribute__((aligned(16))) float vs[F32_BLK][HD];
-    __shared__ __attribute__((aligned(16))) float ps[F32_SLOTS][F32_BLK + 4];  // rows 16-byte aligned
-    __shared__ float corr_s[F32_SLOTS], fa[F32_SLOTS], fb[F32_SLOTS], lsum[F32_SLOTS];
     __shared__ uint32_t tail[MAX_ITEMS];
 
     const uint32_t tid = threadIdx.x;
@@ -108,17 +110,21 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
             v = p.q[((size_t)r * p.nh + h) * hd + d];
         }
-        qs[n][(d % 8) * JS + d / 8] = v;
+        qs[n][(d % 8) * NI + d / 8] = v;
     }
 
-    float o[NP], R[NP];
+    const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Slot wave + W s's running state: m, l, and the folded RM, RL (wave-uniform), and its
+    // dims lane * DPL .. + DPL - 1 of o and R.
+    float m[SPW], l[SPW], RM[SPW], RL[SPW], o[SPW][DPL], R[SPW][DPL];
 #pragma unroll
-    for (int i = 0; i < NP; i++) o[i] = R[i] = 0.0f;
-    // Slot n's running state: m in lanes 4n .. 4n + 3 of wave 0 (the softmax's lanes of the
-    // slot), l, RM and RL in lane 4n.
-    float m = -INFINITY, l = 0.0f, RM = -INFINITY, RL = 0.0f;
-    const bool slot_lane = tid < 4u * F32_SLOTS && (tid & 3u) == 0u;
-    const uint32_t sn = tid >> 2;  // the slot of a softmax lane
+    for (int s = 0; s < SPW; s++) {
+        m[s] = RM[s] = -INFINITY;
+        l[s] = RL[s] = 0.0f;
+#pragma unroll
+        for (int dd = 0; dd < DPL; dd++) o[s][dd] = R[s][dd] = 0.0f;
+    }
+    const uint32_t dl = lane % DL;  // this lane's dims in P v: dl * DPL .. (lanes past DL repeat them)
 
     // This thread's share of a block's K and V rows (NL 16-byte pieces of each), loaded one
     // block ahead: the next block's loads are in flight while this block computes. Entries
@@ -144,19 +150,29 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
 #pragma unroll
         for (int i = 0; i < NL; i++) {
             const uint32_t e = tid + F32_THREADS * i, k = e / (HD / 4), d = 4 * (e % (HD / 4));
-            float* kd = &ks[k][(d % 8) * JS + d / 8];  // d % 8 is 0 or 4: elements d .. d + 3 are lanes' runs apart
+            float* kd = &ks[k][(d % 8) * NI + d / 8];  // d % 8 is 0 or 4: elements d .. d + 3 are lanes' runs apart
             kd[0] = kr[i][0];
-            kd[JS] = kr[i][1];
-            kd[2 * JS] = kr[i][2];
-            kd[3 * JS] = kr[i][3];
+            kd[NI] = kr[i][1];
+            kd[2 * NI] = kr[i][2];
+            kd[3 * NI] = kr[i][3];
             *(f32x4*)&vs[k][d] = vr[i];
         }
     };
-    // Scores: slot by slot, thread (entry qk, lane qj) sums q[d] k[d] over d = qj, qj + 8, ...
-    // in order (quant::dot's lane qj), and lane 0 of each eight adds the eight sums to 0 in
-    // lane order (row shifts within the 16-lane row).
-    const uint32_t qk = tid >> 3, qj = tid & 7;
     const uint32_t nused = used_e / HD;  // slots that may hold a query
+    // Cross-lane moves: the value 32 lanes up; the max over 16- and 32-lane groups.
+    auto up32 = [](float x) {
+        return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+    };
+    auto wave_max = [](float x) {
+        x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false)));  // row_ror:8
+        x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false)));  // row_ror:4
+        x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xf, 0xf, false)));  // row_ror:2
+        x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false)));  // row_ror:1
+        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    };
 
     const uint32_t cend = p.split ? c_one + 1u : max(1u, (maxlen + CHUNK_MULTI - 1u) / CHUNK_MULTI);
     for (uint32_t c = c_one; c < cend; c++) {
@@ -171,138 +187,111 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            // Scores of (slot, entry) pairs: quant::dot's eight lane sums, then times sc;
-            // entries at or past a slot's list are -inf.
-            // Two slots at a time (each K value read once for both; a slot past nused computes
-            // on zeros and is not written); the lane's steps unrolled over HD, so its LDS reads
-            // go out ahead of the sums that take them.
-            auto lane_sum = [&](float acc) {  // lane 0 of each eight: 0 + acc_0 + ... + acc_7
-                const int ai = __float_as_int(acc);
-                float dsum = 0.0f + acc;
-                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x101, 0xf, 0xf, false));
-                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x102, 0xf, 0xf, false));
-                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x103, 0xf, 0xf, false));
-                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x104, 0xf, 0xf, false));
-                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x105, 0xf, 0xf, false));
-                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x106, 0xf, 0xf, false));
-                dsum += __int_as_float(__builtin_amdgcn_update_dpp(0, ai, 0x107, 0xf, 0xf, false));
-                return dsum;
-            };
-            for (uint32_t n = 0; n < nused; n += 2) {
-                float acc0 = 0.0f, acc1 = 0.0f;
+            // Per slot of this wave: scores, softmax and P v. Lane k < 32 and lane k + 32 take
+            // entry k: each sums quant::dot's lanes 4h .. 4h + 3 (h its half) over their
+            // elements in order, and lane k adds the eight to 0 in lane order (the upper four
+            // from lane k + 32), times sc; -inf at or past the slot's list. The block's max
+            // across the wave; P of entry k in lane k; the block sum and P v entry by entry
+            // in order, P taken from its lane.
+            const uint32_t k = lane & 31u, h = lane >> 5;
 #pragma unroll
+            for (int sw = 0; sw < SPW; sw++) {
+                const uint32_t n = wave + W * sw;
+                if (n >= nused) break;
+                float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
                 for (uint32_t i = 0; i < (uint32_t)NI; i += 4) {
-                    const f32x4 kv = *(const f32x4*)&ks[qk][qj * JS + i];
-                    const f32x4 q0 = *(const f32x4*)&qs[n][qj * JS + i];
-                    const f32x4 q1 = *(const f32x4*)&qs[n + 1][qj * JS + i];
 #pragma unroll
-                    for (uint32_t t = 0; t < 4; t++) {
-                        if (8 * (i + t) < hd) {  // d = qj + 8 (i + t) in order; past hd nothing
-                            acc0 += q0[t] * kv[t];
-                            acc1 += q1[t] * kv[t];
-                        }
+                    for (uint32_t jj = 0; jj < 4; jj++) {
+                        const uint32_t j = 4 * h + jj;
+                        const f32x4 kv = *(const f32x4*)&ks[k][j * NI + i];
+                        const f32x4 qv = *(const f32x4*)&qs[n][j * NI + i];
+#pragma unroll
+                        for (uint32_t t = 0; t < 4; t++)
+                            if (8 * (i + t) < hd) a[jj] += qv[t] * kv[t];  // d = j + 8 (i + t) in order
                     }
                 }
-                const float s0 = lane_sum(acc0), s1 = lane_sum(acc1);
-                if (qj == 0) {
-                    ps[n][qk] = (key0 + qk < slot_len(n)) ? s0 * p.sc : -INFINITY;
-                    if (n + 1 < nused) ps[n + 1][qk] = (key0 + qk < slot_len(n + 1)) ? s1 * p.sc : -INFINITY;
-                }
-            }
-            for (uint32_t e = nused * F32_BLK + tid; e < F32_SLOTS * F32_BLK; e += F32_THREADS)
-                ps[e / F32_BLK][e % F32_BLK] = -INFINITY;
-            __syncthreads();
-            // Per slot: the block's max, the new running max, P and the block's sum of P.
-            // Lanes 4n .. 4n + 3 of wave 0 take slot n's entries eight each: the block's max
-            // across the four (a max is exact in any order), P in parallel, and the block's
-            // sum in entry order by lane 4n (its own eight, then the others' from LDS).
-            static_assert(F32_BLK == 32 && 4 * F32_SLOTS == 64, "wave 0 holds every slot's softmax");
-            if (tid < 4u * F32_SLOTS) {
-                const uint32_t k0 = 8 * (tid & 3u);
-                f32x4 pa = *(const f32x4*)&ps[sn][k0], pb = *(const f32x4*)&ps[sn][k0 + 4];
-                float mx = fmaxf(fmaxf(fmaxf(pa[0], pa[1]), fmaxf(pa[2], pa[3])), fmaxf(fmaxf(pb[0], pb[1]), fmaxf(pb[2], pb[3])));
-                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0xB1, 0xf, 0xf, false)));
-                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x4E, 0xf, 0xf, false)));
-                const float mn = fmaxf(m, mx), ms = (mn == -INFINITY) ? 0.0f : mn;
-                const float cr = exp2_hw(m - ms);
+                float dsum = 0.0f + a[0];
+                dsum += a[1];
+                dsum += a[2];
+                dsum += a[3];
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    pa[t] = exp2_hw(pa[t] - ms);
-                    pb[t] = exp2_hw(pb[t] - ms);
-                }
-                *(f32x4*)&ps[sn][k0] = pa;
-                *(f32x4*)&ps[sn][k0 + 4] = pb;
-                if ((tid & 3u) == 0u) {
-                    float bl = 0.0f;
+                for (int jj = 0; jj < 4; jj++) dsum += up32(a[jj]);
+                const float sc = (lane < 32u && key0 + k < slot_len(n)) ? dsum * p.sc : -INFINITY;
+                const float mx = wave_max(sc);
+                const float mn = fmaxf(m[sw], mx), ms = (mn == -INFINITY) ? 0.0f : mn;
+                const float cr = exp2_hw(m[sw] - ms);
+                const float pe = exp2_hw(sc - ms);
+                float bl = 0.0f, acc[DPL];
 #pragma unroll
-                    for (int t = 0; t < 4; t++) bl += pa[t];
+                for (int dd = 0; dd < DPL; dd++) acc[dd] = 0.0f;
+#pragma unroll 1
+                for (int k8 = 0; k8 < F32_BLK; k8 += 8) {
 #pragma unroll
-                    for (int t = 0; t < 4; t++) bl += pb[t];
+                for (int kj = 0; kj < 8; kj++) {
+                    const int kk = k8 + kj;
+                    const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), kk));
+                    bl += pk;
+                    if constexpr (DPL == 1) {
+                        acc[0] += pk * vs[kk][dl];
+                    } else if constexpr (DPL == 2) {
+                        const float2 v = *(const float2*)&vs[kk][2 * dl];
+                        acc[0] += pk * v.x;
+                        acc[1] += pk * v.y;
+                    } else {
+                        const f32x4 v = *(const f32x4*)&vs[kk][4 * dl];
 #pragma unroll
-                    for (int k = 8; k < F32_BLK; k += 4) {
-                        const f32x4 c = *(const f32x4*)&ps[sn][k];
-                        bl += c[0];
-                        bl += c[1];
-                        bl += c[2];
-                        bl += c[3];
+                        for (int dd = 0; dd < 4; dd++) acc[dd] += pk * v[dd];
                     }
-                    l = l * cr + bl;
-                    corr_s[sn] = cr;
                 }
-                m = mn;
-            }
-            __syncthreads();
-            // O = O * corr + sum of P v, the sum in entry order.
+                }
+                l[sw] = l[sw] * cr + bl;
+                m[sw] = mn;
 #pragma unroll
-            for (int i = 0; i < NP; i++) {
-                const uint32_t e = tid + F32_THREADS * i, n = e / HD, d = e % HD;
-                if (F32_THREADS * i >= used_e) break;
-                float acc = 0.0f;
-                for (int k = 0; k < F32_BLK; k++) acc += ps[n][k] * vs[k][d];
-                o[i] = o[i] * corr_s[n] + acc;
+                for (int dd = 0; dd < DPL; dd++) o[sw][dd] = o[sw][dd] * cr + acc[dd];
             }
         }
         if (p.split) break;
         // The chunk's state folded into the running one (merge_coef, R = R a + c b).
-        if (slot_lane) {
-            float a, b, mn;
-            merge_coef(RM, m, a, b, mn);
-            RL = RL * a + l * b;
-            RM = mn;
-            fa[sn] = a;
-            fb[sn] = b;
-        }
-        m = -INFINITY;
-        l = 0.0f;
-        __syncthreads();
 #pragma unroll
-        for (int i = 0; i < NP; i++) {
-            const uint32_t n = (tid + F32_THREADS * i) / HD;
-            if (F32_THREADS * i >= used_e) break;
-            R[i] = R[i] * fa[n] + o[i] * fb[n];
-            o[i] = 0.0f;
+        for (int sw = 0; sw < SPW; sw++) {
+            float fa, fb, mn;
+            merge_coef(RM[sw], m[sw], fa, fb, mn);
+            RL[sw] = RL[sw] * fa + l[sw] * fb;
+            RM[sw] = mn;
+#pragma unroll
+            for (int dd = 0; dd < DPL; dd++) {
+                R[sw][dd] = R[sw][dd] * fa + o[sw][dd] * fb;
+                o[sw][dd] = 0.0f;
+            }
+            m[sw] = -INFINITY;
+            l[sw] = 0.0f;
         }
-        __syncthreads();  // fa and fb are read before the next chunk's fold writes them
     }
     if (p.split) {
         const size_t u = (size_t)grp * p.nchunk + c_one;
 #pragma unroll
-        for (int i = 0; i < NP; i++) {
-            const uint32_t e = tid + F32_THREADS * i, n = e / HD, d = e % HD;
-            if (F32_THREADS * i >= used_e) break;  // attn_combine reads no slot past them
-            p.part_o[(u * F32_SLOTS + n) * HD + d] = o[i];
+        for (int sw = 0; sw < SPW; sw++) {
+            const uint32_t n = wave + W * sw;
+            if (n >= nused) break;  // attn_combine reads no slot past them
+            if (lane < (uint32_t)DL) {
+#pragma unroll
+                for (int dd = 0; dd < DPL; dd++) p.part_o[(u * F32_SLOTS + n) * HD + DPL * dl + dd] = o[sw][dd];
+            }
+            if (lane == 0) *(float2*)(p.part_ml + (u * F32_SLOTS + n) * 2) = float2{m[sw], l[sw]};
         }
-        if (slot_lane) *(float2*)(p.part_ml + (u * F32_SLOTS + sn) * 2) = float2{m, l};
         return;
     }
-    if (slot_lane) lsum[sn] = RL;
-    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < NP; i++) {
-        const uint32_t e = tid + F32_THREADS * i, n = e / HD, d = e % HD;
-        if (d < hd && slot_valid(n)) {
-            const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
-            p.out[((size_t)r * p.nh + h) * hd + d] = R[i] / lsum[n];
+    for (int sw = 0; sw < SPW; sw++) {
+        const uint32_t n = wave + W * sw;
+        if (n >= nused) break;
+        if (!slot_valid(n) || lane >= (uint32_t)DL) continue;
+        const uint32_t r = r0 + n % p.rb, hh = kvh * p.G + n / p.rb;
+#pragma unroll
+        for (int dd = 0; dd < DPL; dd++) {
+            const uint32_t d = DPL * dl + dd;
+            if (d < hd) p.out[((size_t)r * p.nh + hh) * hd + d] = R[sw][dd] / RL[sw];
         }
     }
 }
