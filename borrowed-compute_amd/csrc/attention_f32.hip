@@ -103,15 +103,6 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     // products, the folds and the stores skip them, whole iterations at a time (uniform).
     const uint32_t used_e = min((uint32_t)F32_SLOTS, p.G * p.rb) * HD;
 
-    for (uint32_t e = tid; e < F32_SLOTS * HD; e += F32_THREADS) {
-        const uint32_t n = e / HD, d = e % HD;
-        float v = 0.0f;
-        if (d < hd && slot_valid(n)) {
-            const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
-            v = p.q[((size_t)r * p.nh + h) * hd + d];
-        }
-        qs[n][(d % 8) * NI + d / 8] = v;
-    }
 
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Slot wave + W s's running state: m, l, and the folded RM, RL (wave-uniform), and its
@@ -174,14 +165,33 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
         return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     };
 
+    // The first block's loads go out before q is staged, so that the two latencies overlap
+    // (a tree's loads name slots from tail: every thread's entries of it are in first). Each
+    // chunk's last block loads the next chunk's first (chunks past the list are empty, and
+    // only they).
+    if (p.tree) __syncthreads();
     const uint32_t cend = p.split ? c_one + 1u : max(1u, (maxlen + CHUNK_MULTI - 1u) / CHUNK_MULTI);
+    if (c_one * CHUNK_MULTI < maxlen) fetch(c_one * CHUNK_MULTI, min(c_one * CHUNK_MULTI + CHUNK_MULTI, maxlen));
+    for (uint32_t e = tid; e < F32_SLOTS * HD; e += F32_THREADS) {
+        const uint32_t n = e / HD, d = e % HD;
+        float v = 0.0f;
+        if (d < hd && slot_valid(n)) {
+            const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
+            v = p.q[((size_t)r * p.nh + h) * hd + d];
+        }
+        qs[n][(d % 8) * NI + d / 8] = v;
+    }
     for (uint32_t c = c_one; c < cend; c++) {
         const uint32_t kb0 = c * CHUNK_MULTI, kb1 = min(kb0 + CHUNK_MULTI, maxlen);
-        if (kb0 < kb1) fetch(kb0, kb1);
         for (uint32_t key0 = kb0; key0 < kb1; key0 += F32_BLK) {
             __syncthreads();  // the previous block's K, V and P are consumed (and q is in)
             stash();
-            if (key0 + F32_BLK < kb1) fetch(key0 + F32_BLK, kb1);
+            if (key0 + F32_BLK < kb1) {
+                fetch(key0 + F32_BLK, kb1);
+            } else if (c + 1 < cend && kb1 < maxlen) {
+                const uint32_t nb0 = (c + 1) * CHUNK_MULTI;
+                fetch(nb0, min(nb0 + CHUNK_MULTI, maxlen));
+            }
             // K and V in for everyone. The fences order LDS only: __syncthreads' would also
             // wait for the next block's loads just issued.
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
