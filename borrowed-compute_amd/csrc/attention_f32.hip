@@ -209,18 +209,25 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
                 const uint32_t n = wave + W * sw;
                 if (n >= nused) break;
                 float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                // d = j + 8 (i + t) in order; past hd (a head dim below HD) no term.
+                auto dot_lanes = [&](auto FULL) {
 #pragma unroll 1
-                for (uint32_t i = 0; i < (uint32_t)NI; i += 4) {
+                    for (uint32_t i = 0; i < (uint32_t)NI; i += 4) {
 #pragma unroll
-                    for (uint32_t jj = 0; jj < 4; jj++) {
-                        const uint32_t j = 4 * h + jj;
-                        const f32x4 kv = *(const f32x4*)&ks[k][j * NI + i];
-                        const f32x4 qv = *(const f32x4*)&qs[n][j * NI + i];
+                        for (uint32_t jj = 0; jj < 4; jj++) {
+                            const uint32_t j = 4 * h + jj;
+                            const f32x4 kv = *(const f32x4*)&ks[k][j * NI + i];
+                            const f32x4 qv = *(const f32x4*)&qs[n][j * NI + i];
 #pragma unroll
-                        for (uint32_t t = 0; t < 4; t++)
-                            if (8 * (i + t) < hd) a[jj] += qv[t] * kv[t];  // d = j + 8 (i + t) in order
+                            for (uint32_t t = 0; t < 4; t++)
+                                if (decltype(FULL)::value || 8 * (i + t) < hd) a[jj] += qv[t] * kv[t];
+                        }
                     }
-                }
+                };
+                if (hd == (uint32_t)HD)
+                    dot_lanes(std::true_type{});
+                else
+                    dot_lanes(std::false_type{});
                 float dsum = 0.0f + a[0];
                 dsum += a[1];
                 dsum += a[2];
