@@ -33,6 +33,7 @@
 
 #include <hip/hip_ext.h>
 #include <math.h>
+#include <algorithm>
 #include <type_traits>
 #include <stdlib.h>
 
@@ -561,11 +562,18 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 && HD <= 128 ? 4 : 2) void at
 // finish, found by an arrival counter, would save that launch, but publishing each state
 // takes a device-scope release, an L2 write-back per workgroup: measured at +8 us for 256
 // workgroups and +175 us for 4096 on MI355X.)
+// The fold's order is fixed by the list alone: runs of ROW_RUN consecutive chunks, each
+// folded left to right from a cleared state, then attn_row_fold's order over the runs. A
+// launch of many units (RUNS: a ragged batch, whose lists keep the chunks they would have
+// alone) gives each wave a whole run: it folds the run's chunks itself, in that order, and
+// writes one state a run (a quarter of the states written and read back); the bits are
+// those of a unit a chunk.
 constexpr int RB = 32;                     // list entries per block of the one-row kernel
 constexpr uint32_t ROW_FUSE_MAXG = 8;      // query heads per KV head a fused step takes
 constexpr uint32_t ROW_MAX_CHUNKS = 256;   // chunks per (item, KV head): attn_row_fold's reach
+constexpr uint32_t ROW_RUN = 4;            // chunks a run
 
-template <int HD, typename KVT, bool FUSE>
+template <int HD, typename KVT, bool FUSE, bool RUNS>
 __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) {
     constexpr int NKC = HD / 32;        // hd chunks of a score MFMA
     constexpr int NDT = HD / 16;        // output tiles of 16 dims
@@ -612,15 +620,26 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         I = p.items[it];
     }
     const uint32_t pos0 = FUSE ? p.positions[I.row] : 0u;  // before any store: a scalar load
-    const uint32_t rem = u - I.unit0, c = rem / p.nkv, kvh = rem % p.nkv;
-    const uint32_t kb0 = c * I.chunk, kb1 = min(kb0 + I.chunk, I.len);
+    // The unit's chunks: one (uu), or with RUNS run uu's chunks cfirst .. cend - 1.
+    const uint32_t rem = u - I.unit0, uu = rem / p.nkv, kvh = rem % p.nkv;
+    const uint32_t cfirst = RUNS ? uu * ROW_RUN : uu;
+    const uint32_t cend = RUNS ? min(cfirst + ROW_RUN, I.nchunk) : cfirst + 1;
     // The last chunk streams up to the list's last entry and then takes that entry alone:
     // the same blocks whether the entry came from the cache or, in a fused step, from this
     // kernel's own rotation (so both give the same bits), and no block of the stream holds a
     // slot this kernel writes.
     const uint32_t last = I.len - 1;
-    const bool has_last = kb1 == I.len;
-    const uint32_t kbs = has_last ? last : kb1;  // end of the streamed entries
+    const bool unit_last = min(cend * I.chunk, I.len) == I.len;  // the unit takes the list's last chunk
+    // The chunk being streamed: its entries kb0 .. kb1 - 1, streamed up to kbs.
+    uint32_t kb0, kb1, kbs;
+    bool has_last;
+    auto set_chunk = [&](uint32_t c) {
+        kb0 = c * I.chunk;
+        kb1 = min(kb0 + I.chunk, I.len);
+        has_last = kb1 == I.len;
+        kbs = has_last ? last : kb1;
+    };
+    set_chunk(cfirst);
     const bool valid = (uint32_t)n < G;
     const KVT* zp = (const KVT*)p.zero;
     const KVT* kc = (const KVT*)p.kc + I.kvoff * kvd + (size_t)kvh * hd;
@@ -665,7 +684,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     // of a fused step then runs while the blocks are in flight.
     half8 qb[NKC];  // Q^T operands (B of the score MFMAs)
     f16* vw = vl[w];
-    const bool has_new = FUSE && has_last;  // this chunk writes the new row
+    const bool has_new = FUSE && unit_last;  // this unit writes the new row
     constexpr bool DB = sizeof(KVT) == 2 && HD <= 128;
     constexpr int NLE = (HD + 63) / 64;                              // row elements per lane
     constexpr int NPJ = (HD / 2 + 63) / 64;                          // RoPE pairs per lane
@@ -703,7 +722,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
 #pragma unroll
         for (int j = 0; j < NLE; j++) {
             const uint32_t e = lane + 64 * j;
-            const bool ok = has_last && e < hd;
+            const bool ok = unit_last && e < hd;
             lk[j] = *(ok ? kc + (size_t)last * kvd + e : zp);
             lv[j] = *(ok ? vc + (size_t)last * kvd + e : zp);
         }
@@ -719,13 +738,17 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     Raw<KVT> kR[2][2][NKC], vR[NVL], vR2[NVL];
     // A stream of at most two blocks (short lists) has all of it in flight through the
     // prologue; a longer one has the first block and the second block's K.
-    const bool two = kbs <= kb0 + 2 * RB;
-    if constexpr (DB) {
-        load_k(kb0, kR[0]);
-        load_v(kb0, vR);
-        load_k(kb0 + RB, kR[1]);
-        if (two) load_v(kb0 + RB, vR2);
-    }
+    bool two;
+    auto first_loads = [&]() {
+        two = kbs <= kb0 + 2 * RB;
+        if constexpr (DB) {
+            load_k(kb0, kR[0]);
+            load_v(kb0, vR);
+            load_k(kb0 + RB, kR[1]);
+            if (two) load_v(kb0 + RB, vR2);
+        }
+    };
+    first_loads();
     if constexpr (FUSE) {
         // q, k and v into the LDS tile; then each lane rotates its pairs there (the angle
         // depends on the pair alone, so its sine and cosine serve all G heads and the new K
@@ -808,7 +831,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
         // reading it, so with several chunks the first one stages the rotated heads (at the
         // item's place in qrot) and attn_row_fold, which runs after every unit, copies them
         // into q; a lone unit writes q.
-        if (c == 0) {
+        if (cfirst == 0) {
             float* dst = (I.nchunk == 1 ? p.qw + (size_t)I.row * p.nh * hd : p.qrot + (size_t)it * p.nh * hd) +
                          (size_t)kvh * G * hd;
             for (uint32_t e = 4 * lane; e < G * hd; e += 256)
@@ -817,7 +840,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     } else {
 #pragma unroll
         for (int c2 = 0; c2 < NKC; c2++) qb[c2] = q_scaled(qa[c2], qc[c2], p.sc);
-        if (has_last) {
+        if (unit_last) {
 #pragma unroll
             for (int j = 0; j < NLE; j++) {
                 const uint32_t e = lane + 64 * j;
@@ -895,53 +918,92 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     // prefetch measured slower (more requests in flight than the memory system serves
     // best). Wider rows load and compute one block at a time; the other resident waves of
     // the CU still overlap them.
-    if constexpr (DB) {
-        // The first block, then two blocks per trip and one exit, at the bottom: with an exit
-        // after every block the compiler merges the exits into one block that also leads back
-        // to the loop's top, and must then assume loads of every register set are still in
-        // flight there. A chunk with an even block count computes one block past its end: its
-        // entries are all masked (P = 0 exactly, the max and the scale hold), its loads read
-        // the zero page, and the state comes out unchanged.
-        if (two) {
-            compute_block(kb0, kbs, kR[0], vR, nothing);
-            if (kb0 + RB < kbs) compute_block(kb0 + RB, kbs, kR[1], vR2, nothing);
+    // The streamed chunk's blocks, then (the list's last chunk) its last entry.
+    auto stream = [&]() {
+        if constexpr (DB) {
+            // The first block, then two blocks per trip and one exit, at the bottom: with an exit
+            // after every block the compiler merges the exits into one block that also leads back
+            // to the loop's top, and must then assume loads of every register set are still in
+            // flight there. A chunk with an even block count computes one block past its end: its
+            // entries are all masked (P = 0 exactly, the max and the scale hold), its loads read
+            // the zero page, and the state comes out unchanged.
+            if (two) {
+                compute_block(kb0, kbs, kR[0], vR, nothing);
+                if (kb0 + RB < kbs) compute_block(kb0 + RB, kbs, kR[1], vR2, nothing);
+            } else {
+                compute_block(kb0, kbs, kR[0], vR, [&] { load_v(kb0 + RB, vR); });
+            }
+            for (uint32_t key0 = two ? kbs : kb0 + RB; key0 < kbs; key0 += 2 * RB) {
+    #pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const uint32_t kb = key0 + s * RB;
+                    load_k(kb + RB, kR[s]);
+                    compute_block(kb, kbs, kR[1 - s], vR, [&] { load_v(kb + RB, vR); });
+                }
+            }
         } else {
-            compute_block(kb0, kbs, kR[0], vR, [&] { load_v(kb0 + RB, vR); });
-        }
-        for (uint32_t key0 = two ? kbs : kb0 + RB; key0 < kbs; key0 += 2 * RB) {
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const uint32_t kb = key0 + s * RB;
-                load_k(kb + RB, kR[s]);
-                compute_block(kb, kbs, kR[1 - s], vR, [&] { load_v(kb + RB, vR); });
+            for (uint32_t key0 = kb0; key0 < kbs; key0 += RB) {
+                load_k(key0, kR[0]);
+                load_v(key0, vR);
+                compute_block(key0, kbs, kR[0], vR, nothing);
             }
         }
-    } else {
-        for (uint32_t key0 = kb0; key0 < kbs; key0 += RB) {
-            load_k(key0, kR[0]);
-            load_v(key0, vR);
-            compute_block(key0, kbs, kR[0], vR, nothing);
-        }
-    }
-    if (has_last) {
-        // The last entry as a block of its own: every K row of the block is that entry (the
-        // rows past it are masked), V rows past it are zero.
-        Raw<KVT> kx[2][NKC], vx[NVL];
-        if constexpr (KL) {
-#pragma unroll
-            for (int i = 0; i < NVL; i++) kx[i / NKC][i % NKC].load(&lrow[w][0][8 * (lane % VLR)]);
-        } else {
-#pragma unroll
-            for (int c2 = 0; c2 < NKC; c2++) {
-                kx[0][c2].load(&lrow[w][0][32 * c2 + 8 * g]);
-                kx[1][c2] = kx[0][c2];
+        if (has_last) {
+            // The last entry as a block of its own: every K row of the block is that entry (the
+            // rows past it are masked), V rows past it are zero.
+            Raw<KVT> kx[2][NKC], vx[NVL];
+            if constexpr (KL) {
+    #pragma unroll
+                for (int i = 0; i < NVL; i++) kx[i / NKC][i % NKC].load(&lrow[w][0][8 * (lane % VLR)]);
+            } else {
+    #pragma unroll
+                for (int c2 = 0; c2 < NKC; c2++) {
+                    kx[0][c2].load(&lrow[w][0][32 * c2 + 8 * g]);
+                    kx[1][c2] = kx[0][c2];
+                }
             }
+            vx[0].load(&lrow[w][1][8 * (lane % VLR)]);
+            if (lane >= VLR) vx[0].set(float4{0.0f, 0.0f, 0.0f, 0.0f}, float4{0.0f, 0.0f, 0.0f, 0.0f});
+    #pragma unroll
+            for (int i = 1; i < NVL; i++) vx[i].set(float4{0.0f, 0.0f, 0.0f, 0.0f}, float4{0.0f, 0.0f, 0.0f, 0.0f});
+            compute_block(last, I.len, kx, vx, nothing);
         }
-        vx[0].load(&lrow[w][1][8 * (lane % VLR)]);
-        if (lane >= VLR) vx[0].set(float4{0.0f, 0.0f, 0.0f, 0.0f}, float4{0.0f, 0.0f, 0.0f, 0.0f});
+    };
+    stream();
+    if constexpr (RUNS) {
+        if (I.nchunk > 1) {
+            // The run's state: its chunks folded left to right from a cleared state, with
+            // attn_row_fold's expressions (a run's fold there, when each chunk is a unit).
+            float Mr = -INFINITY, Lr = 0.0f;
+            f32x4 Or[NDT];
 #pragma unroll
-        for (int i = 1; i < NVL; i++) vx[i].set(float4{0.0f, 0.0f, 0.0f, 0.0f}, float4{0.0f, 0.0f, 0.0f, 0.0f});
-        compute_block(last, I.len, kx, vx, nothing);
+            for (int dt = 0; dt < NDT; dt++) Or[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            auto merge_chunk = [&]() {
+                float a, b, mn;
+                merge_coef(Mr, m, a, b, mn);
+                Lr = Lr * a + l * b;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) Or[dt][i] = Or[dt][i] * a + o[dt][i] * b;
+                Mr = mn;
+            };
+            merge_chunk();
+            for (uint32_t c = cfirst + 1; c < cend; c++) {
+                set_chunk(c);
+                first_loads();
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                m = -INFINITY;
+                l = 0.0f;
+                stream();
+                merge_chunk();
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) o[dt] = Or[dt];
+            m = Mr;
+            l = Lr;
+        }
     }
     if (!valid) return;
     if (I.nchunk == 1) {
@@ -952,9 +1014,10 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
             if (d < hd) *(float4*)(orow + d) = float4{o[dt][0] / l, o[dt][1] / l, o[dt][2] / l, o[dt][3] / l};
         }
     } else {
-        // State at the canonical index of (item, KV head, chunk): a group's chunks are
+        // State at the canonical index of (item, KV head, chunk or run): a list's states are
         // contiguous for the fold.
-        const size_t at = ((size_t)I.unit0 + (size_t)kvh * I.nchunk + c) * 16 + n;
+        const uint32_t nst = RUNS ? (I.nchunk + ROW_RUN - 1) / ROW_RUN : I.nchunk;
+        const size_t at = ((size_t)I.unit0 + (size_t)kvh * nst + uu) * 16 + n;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             const uint32_t d = 16 * dt + 4 * g;
@@ -964,45 +1027,71 @@ __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) 
     }
 }
 
+// One state folded into another: (M, L, O) <- fold((M, L, O), (m2, l2, o2)), four dims.
+__device__ __forceinline__ void merge_state(float& M, float& L, float4& O, float m2, float l2, float4 o2) {
+    float a, bb, mn;
+    merge_coef(M, m2, a, bb, mn);
+    L = L * a + l2 * bb;
+    O = float4{O.x * a + o2.x * bb, O.y * a + o2.y * bb, O.z * a + o2.z * bb, O.w * a + o2.w * bb};
+    M = mn;
+}
+
 // The fold of a one-row list's chunk states: a workgroup of ROW_FOLD_THREADS per (item, KV
-// head, slot, ROW_FOLD_DIMS dims), so the loads spread over many CUs. R thread subsets of
-// ROW_FOLD_DIMS / 4 threads (four dims each): subset r folds chunks r, r + R, r + 2R, ...
-// in that order from a cleared state (all its loads issued before the first use), then the
-// R subset states merge as a binary tree (r with r + 1, then r with r + 2, ...) and the root
-// is normalised. The order is fixed by the chunk count and the shape alone.
+// head, slot, ROW_FOLD_DIMS dims), so the loads spread over many CUs. The chunks go in runs
+// of ROW_RUN consecutive chunks, each run folded left to right from a cleared state: here,
+// or (p.runs) by the decode wave that streamed the run, whose states are then run states.
+// R thread subsets of ROW_FOLD_DIMS / 4 threads (four dims each): subset r folds runs r,
+// r + R, ... in that order from a cleared state (all its loads issued before the first
+// use), then the R subset states merge as a binary tree (r with r + 1, then r with r + 2,
+// ...) and the root is normalised. The order is fixed by the chunk count and the shape
+// alone.
 constexpr int ROW_FOLD_THREADS = 256;
 constexpr int ROW_FOLD_DIMS = 32;
 
 template <int HD>
 __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectParams p) {
-    constexpr uint32_t D4 = ROW_FOLD_DIMS / 4;              // threads per subset: 4 dims each
-    constexpr uint32_t R = ROW_FOLD_THREADS / D4;           // subsets
-    constexpr uint32_t NPT = (ROW_MAX_CHUNKS + R - 1) / R;  // chunks per subset at most
+    constexpr uint32_t D4 = ROW_FOLD_DIMS / 4;                          // threads per subset: 4 dims each
+    constexpr uint32_t R = ROW_FOLD_THREADS / D4;                       // subsets
+    constexpr uint32_t NRS = (ROW_MAX_CHUNKS / ROW_RUN + R - 1) / R;    // runs per subset at most
+    constexpr uint32_t NPT = NRS * ROW_RUN;                             // chunk states per subset at most
     constexpr uint32_t NDS = (HD + ROW_FOLD_DIMS - 1) / ROW_FOLD_DIMS;  // dim slices
+    static_assert(ROW_MAX_CHUNKS % ROW_RUN == 0, "whole runs");
     __shared__ float4 rO[ROW_FOLD_THREADS / 64][D4];
     __shared__ float2 rML[ROW_FOLD_THREADS / 64][D4];
     // The arguments are read before any branch on them (their scalar loads go out together);
     // a launch of one item needs no indexed read of the item.
-    const uint32_t nitems = p.nitems, nkv = p.nkv, G = p.G;
+    const uint32_t nitems = p.nitems, nkv = p.nkv, G = p.G, runs = p.runs;
     Item I = p.items[0];
-    asm volatile("" ::"s"(nitems), "s"(nkv), "s"(G), "s"(I.row), "s"(I.unit0), "s"(I.nchunk), "s"(p.hd), "s"(p.nh),
-                 "s"(p.fuse), "s"(p.out), "s"(p.part_o), "s"(p.part_ml), "s"(p.qw), "s"(p.qrot));
+    asm volatile("" ::"s"(nitems), "s"(nkv), "s"(G), "s"(runs), "s"(I.row), "s"(I.unit0), "s"(I.nchunk), "s"(p.hd),
+                 "s"(p.nh), "s"(p.fuse), "s"(p.out), "s"(p.part_o), "s"(p.part_ml), "s"(p.qw), "s"(p.qrot));
     const uint32_t b = blockIdx.x / NDS, ds = blockIdx.x % NDS, per_item = nkv * G;
     const uint32_t item = b / per_item;
     if (nitems > 1) I = p.items[item];
-    const uint32_t nch = I.nchunk;
+    const uint32_t nch = I.nchunk, nrun = (nch + ROW_RUN - 1) / ROW_RUN;
     if (nch <= 1) return;  // written by the decode kernel
     const uint32_t kvh = (b % per_item) / p.G, s = (b % per_item) % p.G;
     const uint32_t tid = threadIdx.x, r = tid / D4, d = ds * ROW_FOLD_DIMS + 4 * (tid % D4);
-    const size_t cu0 = (size_t)I.unit0 + (size_t)kvh * nch;
+    const size_t st0 = (size_t)I.unit0 + (size_t)kvh * (runs ? nrun : nch);  // the list's first state
+    // State j of this subset's run q (run r + q R): its chunk j, or with runs the run's state
+    // at j = 0.
     float2 ml[NPT];
     float4 ov[NPT];
+    if (runs) {
 #pragma unroll
-    for (uint32_t q = 0; q < NPT; q++) {
-        const uint32_t c = r + q * R;
-        const size_t at = (cu0 + (c < nch ? c : 0u)) * 16 + s;
-        ml[q] = *(const float2*)(p.part_ml + at * 2);
-        ov[q] = *(const float4*)(p.part_o + at * HD + d);
+        for (uint32_t q = 0; q < NRS; q++) {
+            const uint32_t run = r + q * R;
+            const size_t at = (st0 + (run < nrun ? run : 0u)) * 16 + s;
+            ml[q * ROW_RUN] = *(const float2*)(p.part_ml + at * 2);
+            ov[q * ROW_RUN] = *(const float4*)(p.part_o + at * HD + d);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t q = 0; q < NPT; q++) {
+            const uint32_t c = (r + q / ROW_RUN * R) * ROW_RUN + q % ROW_RUN;
+            const size_t at = (st0 + (c < nch ? c : 0u)) * 16 + s;
+            ml[q] = *(const float2*)(p.part_ml + at * 2);
+            ov[q] = *(const float4*)(p.part_o + at * HD + d);
+        }
     }
     // After the state loads are out (a store before them would hold them behind its load).
     if (p.fuse && tid < ROW_FOLD_DIMS && ds * ROW_FOLD_DIMS + tid < p.hd) {
@@ -1013,26 +1102,28 @@ __global__ __launch_bounds__(ROW_FOLD_THREADS) void attn_row_fold(const DirectPa
     float M = -INFINITY, L = 0.0f;
     float4 O = float4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (uint32_t q = 0; q < NPT; q++) {
-        if (r + q * R < nch) {
-            float a, bb, mn;
-            merge_coef(M, ml[q].x, a, bb, mn);
-            L = L * a + ml[q].y * bb;
-            O = float4{O.x * a + ov[q].x * bb, O.y * a + ov[q].y * bb, O.z * a + ov[q].z * bb, O.w * a + ov[q].w * bb};
-            M = mn;
+    for (uint32_t q = 0; q < NRS; q++) {
+        const uint32_t run = r + q * R;
+        if (run < nrun) {
+            float Mq = ml[q * ROW_RUN].x, Lq = ml[q * ROW_RUN].y;
+            float4 Oq = ov[q * ROW_RUN];
+            if (!runs) {
+                Mq = -INFINITY;
+                Lq = 0.0f;
+                Oq = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (uint32_t j = 0; j < ROW_RUN; j++)
+                    if (run * ROW_RUN + j < nch)
+                        merge_state(Mq, Lq, Oq, ml[q * ROW_RUN + j].x, ml[q * ROW_RUN + j].y, ov[q * ROW_RUN + j]);
+            }
+            merge_state(M, L, O, Mq, Lq, Oq);
         }
     }
     // The binary tree over the subsets (r with r + 1, then r with r + 2, ...): its levels
     // within a wave (eight subsets of D4 lanes: partners 8, 16 and 32 lanes up) by cross-lane
     // moves, without a barrier; the two across the workgroup's waves through LDS. A lane
     // whose subset is not a left operand at a level computes a value no one reads.
-    auto merge = [&](float m2, float l2, float4 o2) {
-        float a, bb, mn;
-        merge_coef(M, m2, a, bb, mn);
-        L = L * a + l2 * bb;
-        O = float4{O.x * a + o2.x * bb, O.y * a + o2.y * bb, O.z * a + o2.z * bb, O.w * a + o2.w * bb};
-        M = mn;
-    };
+    auto merge = [&](float m2, float l2, float4 o2) { merge_state(M, L, O, m2, l2, o2); };
     static_assert(D4 == 8 && ROW_FOLD_THREADS == 256, "eight subsets a wave, four waves");
     {
         // partner 8 lanes up: DPP rotation by 8 within each row of 16 lanes
@@ -1696,14 +1787,21 @@ __device__ __forceinline__ void group_fold_slots(const SharedParams& p, uint32_t
 #pragma unroll
         for (uint32_t c = 0; c < MC; c++) o[c] = *(const float2*)(ob + c * HD);
         const float mc = lane < nch ? ml.x : -INFINITY;
-        float pm = mc;  // inclusive prefix max over lanes 0..31
-#pragma unroll
-        for (int d = 1; d < 32; d <<= 1) {
-            const float t = __shfl_up(pm, d);
-            if (lane >= (uint32_t)d) pm = fmaxf(pm, t);
-        }
-        float before = __shfl_up(pm, 1);  // the running max before chunk `lane`
-        if (lane == 0) before = -INFINITY;
+        // Inclusive prefix max over lanes 0..31 by DPP moves (a lane whose source falls
+        // outside the pattern takes -inf, the max's identity): shifts right by 1, 2, 4 and 8
+        // within each row of 16 lanes, then lane 15's max broadcast into row 1; then the
+        // whole wave shifted right by one lane, so lane c holds the max of chunks 0..c-1.
+        auto dpp = [](float x, auto ctrl, auto rows) {
+            return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(x),
+                                                               decltype(ctrl)::value, decltype(rows)::value, 0xf, false));
+        };
+        float pm = mc;
+        pm = fmaxf(pm, dpp(pm, std::integral_constant<int, 0x111>{}, std::integral_constant<int, 0xf>{}));  // row_shr:1
+        pm = fmaxf(pm, dpp(pm, std::integral_constant<int, 0x112>{}, std::integral_constant<int, 0xf>{}));  // row_shr:2
+        pm = fmaxf(pm, dpp(pm, std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xf>{}));  // row_shr:4
+        pm = fmaxf(pm, dpp(pm, std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xf>{}));  // row_shr:8
+        pm = fmaxf(pm, dpp(pm, std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xa>{}));  // row_bcast:15
+        const float before = dpp(pm, std::integral_constant<int, 0x138>{}, std::integral_constant<int, 0xf>{});  // wave_shr:1
         float a, b, mn;
         merge_coef(before, mc, a, b, mn);
         float4* wl = wts + wave * MC;
@@ -2419,10 +2517,14 @@ static hipError_t launch_decode_t(DirectParams& dp, CombineParams& cp, const Att
 template <int HD, typename KVT>
 static hipError_t launch_row_t(const DirectParams& dp, bool fold, const AttnCall& a, hipStream_t s) {
     const dim3 grid(ceil_div(dp.nunits, 4)), block(256);
-    if (dp.fuse)
-        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, true>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
+    if (dp.fuse && dp.runs)
+        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, true, true>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
+    else if (dp.fuse)
+        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, true, false>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
+    else if (dp.runs)
+        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, false, true>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
     else
-        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, false>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
+        hipExtLaunchKernelGGL((attn_decode_row<HD, KVT, false, false>), grid, block, 0, s, a.ev_before, a.ev_after, 0, dp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !fold) return e;
     const uint32_t slices = (HD + ROW_FOLD_DIMS - 1) / ROW_FOLD_DIMS;
@@ -2527,9 +2629,20 @@ static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nite
         I.nrows = 1;
         I.chunk = row_chunk(I.len, a.nkv);
         I.nchunk = ceil_div(I.len, I.chunk);
-        I.unit0 = (uint32_t)units;
         units += (uint64_t)a.nkv * I.nchunk;
         fold = fold || I.nchunk > 1;
+    }
+    // A unit a chunk, or a unit a run of ROW_RUN chunks where that still leaves ROW_UNITS
+    // units or more (a ragged batch of long lists).
+    dp.runs = ws.row_runs == 2 || (ws.row_runs == 1 && units >= ROW_RUN * ROW_UNITS);
+    // The items of the longest chunks first, so that the launch's last workgroups are its
+    // shortest (an item's place in the launch changes none of its arithmetic).
+    std::stable_sort(dp.items, dp.items + nitems, [](const Item& x, const Item& y) { return x.chunk > y.chunk; });
+    units = 0;
+    for (uint32_t i = 0; i < nitems; i++) {
+        Item& I = dp.items[i];
+        I.unit0 = (uint32_t)units;
+        units += (uint64_t)a.nkv * (dp.runs ? ceil_div(I.nchunk, ROW_RUN) : I.nchunk);
     }
     if (units > 0x7fffffffull) return hipErrorInvalidValue;
     dp.nunits = (uint32_t)units;

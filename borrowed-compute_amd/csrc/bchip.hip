@@ -186,6 +186,7 @@ void Workspace::set_fixed(void* base, size_t o_bytes, size_t ml_bytes, size_t q_
     group_spread = owner.group_spread;
     group_spins = owner.group_spins;
     combine_long = owner.combine_long;
+    row_runs = owner.row_runs;
     gerr = owner.gerr;
     gerr_host = owner.gerr_host;
 }
@@ -256,6 +257,7 @@ hipError_t Workspace::init(int device) {
     group_spread = gf && strcmp(gf, "spread") == 0;
     const char* cl = getenv("BCHIP_COMBINE_LONG");
     combine_long = !(cl && strcmp(cl, "0") == 0);
+    if (const char* rr = getenv("BCHIP_ROW_RUNS")) row_runs = strcmp(rr, "0") == 0 ? 0u : strcmp(rr, "2") == 0 ? 2u : 1u;
     if (const char* sp = getenv("BCHIP_GROUP_FOLD_SPINS")) {
         const long v = strtol(sp, nullptr, 10);
         if (v > 0 && v < (1l << 24)) group_spins = (uint32_t)v;

@@ -134,6 +134,9 @@ struct DirectParams {
     const uint32_t* positions;  // positions[0]: the rotation's position
     uint32_t rope_dim, neox;
     float* qrot;                // [nh][hd]: the rotated q, staged for attn_row_fold to copy into qw
+    // One-row launches: each unit takes a run of chunks and writes the run's state (units
+    // and states numbered by run), else a chunk.
+    uint32_t runs;
     uint32_t nitems;
     Item items[MAX_ITEMS];
 };

@@ -31,6 +31,9 @@ struct Workspace {
     // BCHIP_COMBINE_LONG=0 at init: lists of more than CMB_RUN chunks fold in attn_combine
     // as shorter ones do, not in attn_combine_long (the same bits; for tests).
     bool combine_long = true;
+    // BCHIP_ROW_RUNS at init: one-row launches give each unit a run of chunks when they have
+    // many units (1, the default), always (2) or never (0); the same bits (for tests).
+    uint32_t row_runs = 1;
     uint32_t* gerr = nullptr;       // device address of the host word
     volatile uint32_t* gerr_host = nullptr;
     void* vt = nullptr;    // V^T tiles of a prefill call; the sampler's keys and sort scratch
