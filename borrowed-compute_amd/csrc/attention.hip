@@ -2176,68 +2176,121 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     }
 }
 
-// The softmax of a 16-slot tile over a 64-entry block from relative scores: y = s - m, the
-// slot's running max already subtracted by the score MFMAs (their accumulators start at -m),
-// except in a list's first block (first: y = s, and the block's max becomes m). The running
-// max moves only when a block's relative max passes LAZY, and the subtraction of a new max
-// runs only in a wave where some slot's max moved. P = 2^y rounded to f16, its block sum
-// by the dot2 chain as in tile_softmax; corr is the factor O and l take (1 when m held).
-template <int NDT>
-__device__ __forceinline__ void tile_softmax_rel(State<NDT>& s, f32x4 (&y)[4], half8 (&pb)[2], float& corr,
-                                                 bool first) {
-    float my = fmaxf(fmaxf(y[0][0], y[0][1]), fmaxf(y[0][2], y[0][3]));
+// The softmax of NT 16-slot tiles of a wave over one 64-entry block, from relative scores,
+// with tile_softmax_rel's arithmetic per slot but the tiles' steps interleaved (each step of
+// every tile before the next step), so that the tiles' dependency chains overlap in one wave,
+// and one uniform branch for all tiles where tile_softmax_rel has one a tile: subtracting a
+// moved max runs for every tile when a slot of any tile moved (a tile none of whose slots
+// moved subtracts 0, exact), and the rescale of O likewise (its slots multiply by 1, exact).
+// FIRST: the list's first block (no running max yet).
+template <int NDT, int NT, bool FIRST>
+__device__ __forceinline__ void tiles_softmax_rel(State<NDT> (&s)[NT], f32x4 (&y)[NT][4], half8 (&pb)[NT][2]) {
+    float my[NT];
 #pragma unroll
-    for (int kt = 1; kt < 4; kt++) my = fmaxf(my, fmaxf(fmaxf(y[kt][0], y[kt][1]), fmaxf(y[kt][2], y[kt][3])));
-    my = tile_max(my);
-    float ms;
-    bool up;
-    if (first) {
-        ms = (my == -INFINITY) ? 0.0f : my;
-        up = true;
-        corr = 1.0f;  // O and l are still zero
-        s.m = my;
+    for (int t = 0; t < NT; t++) {
+        my[t] = fmaxf(fmaxf(y[t][0][0], y[t][0][1]), fmaxf(y[t][0][2], y[t][0][3]));
+#pragma unroll
+        for (int kt = 1; kt < 4; kt++)
+            my[t] = fmaxf(my[t], fmaxf(fmaxf(y[t][kt][0], y[t][kt][1]), fmaxf(y[t][kt][2], y[t][kt][3])));
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) my[t] = xmax16(my[t]);
+#pragma unroll
+    for (int t = 0; t < NT; t++) my[t] = xmax32(my[t]);
+    float ms[NT], corr[NT];
+    if constexpr (FIRST) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            ms[t] = (my[t] == -INFINITY) ? 0.0f : my[t];
+            corr[t] = 1.0f;  // O and l are still zero
+            s[t].m = my[t];
+        }
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[t][kt][i] = y[t][kt][i] - ms[t];
     } else {
-        up = my > LAZY;
-        ms = up ? my : 0.0f;
-        corr = up ? exp2_hw(-my) : 1.0f;
-        s.m = up ? s.m + my : s.m;
-    }
-    if (__any(up)) {
-        keep_branch();
+        bool any = false;
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
+        for (int t = 0; t < NT; t++) {
+            const bool up = my[t] > LAZY;
+            ms[t] = up ? my[t] : 0.0f;
+            corr[t] = up ? exp2_hw(-my[t]) : 1.0f;
+            s[t].m = up ? s[t].m + my[t] : s[t].m;
+            any = any || up;
+        }
+        if (__any(any)) {
+            keep_branch();
 #pragma unroll
-            for (int i = 0; i < 4; i++) y[kt][i] = y[kt][i] - ms;
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) y[t][kt][i] = y[t][kt][i] - ms[t];
+        }
     }
-    uint32_t hp[4][2];
-    float ls = 0.0f;
+    uint32_t hp[NT][4][2];
+    float ls[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) ls[t] = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const half2 h = half2{(f16)exp2_hw(y[kt][2 * j]), (f16)exp2_hw(y[kt][2 * j + 1])};
-            ls = pair_sum(h, ls);
-            hp[kt][j] = __builtin_bit_cast(uint32_t, h);
-        }
-    const float ps = tile_sum(ls);
-    s.l = s.l * corr + ps;
+        for (int j = 0; j < 2; j++)
 #pragma unroll
-    for (int kc = 0; kc < 2; kc++)
-        pb[kc] = __builtin_bit_cast(half8, u32x4{hp[2 * kc][0], hp[2 * kc][1], hp[2 * kc + 1][0], hp[2 * kc + 1][1]});
+            for (int t = 0; t < NT; t++) {
+                const half2 h = half2{(f16)exp2_hw(y[t][kt][2 * j]), (f16)exp2_hw(y[t][kt][2 * j + 1])};
+                ls[t] = pair_sum(h, ls[t]);
+                hp[t][kt][j] = __builtin_bit_cast(uint32_t, h);
+            }
+    float ps[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) ps[t] = xsum16(ls[t]);
+#pragma unroll
+    for (int t = 0; t < NT; t++) ps[t] = xsum32(ps[t]);
+#pragma unroll
+    for (int t = 0; t < NT; t++) s[t].l = s[t].l * corr[t] + ps[t];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++)
+            pb[t][kc] = __builtin_bit_cast(half8, u32x4{hp[t][2 * kc][0], hp[t][2 * kc][1], hp[t][2 * kc + 1][0],
+                                                        hp[t][2 * kc + 1][1]});
+    if constexpr (!FIRST) {
+        bool same = true;
+#pragma unroll
+        for (int t = 0; t < NT; t++) same = same && corr[t] == 1.0f;
+        if (!__all(same)) {
+            keep_branch();
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) s[t].o[dt] = s[t].o[dt] * corr[t];
+        }
+    }
 }
 
 // Wide line passes (prefill) on f16 caches at hd 128: every row's list in one online softmax
 // over 64-entry blocks from slot 0, one accumulator a slot (no chunk fold). Each wave takes
 // two 16-slot tiles (32 query slots), so every K and V operand read from LDS feeds two
 // MFMAs; a workgroup is four waves (128 slots: rows x the G heads of one KV head), and K and
-// V^T blocks stream HBM -> LDS by direct-to-LDS loads through a ring of two stages (32 KB
-// each), one block ahead. At 64 KB of LDS and at most 256 registers a lane, two workgroups
-// share a CU, one wave of each on every SIMD; the two are not synchronised with each other,
-// so one's softmax runs beside the other's MFMAs.
+// V^T (packed by vt_pack) blocks stream HBM -> LDS by direct-to-LDS loads through a ring of
+// two stages (32 KB each), one block ahead. At 64 KB of LDS and at most 256 registers a lane,
+// two workgroups share a CU, one wave of each on every SIMD; the two are not synchronised
+// with each other, so one's softmax runs beside the other's MFMAs.
 // The arithmetic per slot is block_step's (scores by 16x16x32 f16 MFMAs in log2 units, the
-// lazy running max, P rounded to f16 once, PV into the same accumulator); a row's bits
-// depend only on its q and its list, never on the rows beside it.
-template <bool VT, int NT>
+// lazy running max, P rounded to f16 once, PV into the same accumulator; the score MFMAs'
+// accumulators start at -m, so the running max rides in them); a row's bits depend only on
+// its q and its list, never on the rows beside it.
+// The loop is mostly one wave's chain of dependent steps (scores, softmax, PV), which the
+// other wave on the SIMD hides only in part, so the schedule shortens that chain:
+//  - the K operands are read from LDS two hd chunks ahead of the MFMAs that take them (eight
+//    operands in flight), and the first V^T operands during the last score MFMAs;
+//  - the two tiles' softmax steps interleave (tiles_softmax_rel), one branch for both;
+//  - the list's first block is a copy of its own (no test of it in the loop).
+template <int NT>
 __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
     constexpr int HD = 128;
     constexpr int NKC = HD / 32, NDT = HD / 16, W = 4;
@@ -2245,6 +2298,7 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
     constexpr int LPW = BLK / RPI / W;          // load instructions per wave per block (K or V)
     constexpr int SZ = 2 * BLK * HD;            // f16 per stage: K rows, then V (or V^T)
     static_assert(LPW * RPI * W == BLK, "a block's rows divide over the waves");
+    static_assert(NKC == 4, "the score phase below reads K two hd chunks ahead of four");
     __shared__ __attribute__((aligned(16))) f16 ring0[SZ];
     __shared__ __attribute__((aligned(16))) f16 ring1[SZ];
 
@@ -2258,8 +2312,6 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
     const uint32_t maxlen = p.pos + rlast + 1u;
     const uint32_t kvd = p.nkv * HD;
 
-    // Slot n of tile t of this wave is slot 32w + 16t + n of the workgroup: head gh, row
-    // r0 + rl. Its Q is loaded here and converted once the first block's loads are out.
     half8 qb[NT][NKC];
     float4 qraw[NT][NKC][2];
     uint32_t len[NT], orow[NT], ohead[NT];
@@ -2283,43 +2335,37 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
 
     const f16* zp = (const f16*)p.zero;
     const f16* kcb = (const f16*)p.kc + (size_t)kvh * HD;
-    const f16* vcb = VT ? (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad : (const f16*)p.vc + (size_t)kvh * HD;
+    const f16* vcb = (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad;
     uint32_t krow[LPW], koff[LPW], voff[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
         const uint32_t q = i * W + w, row = q * RPI + lane / PF_CPR, pch = lane % PF_CPR;
         krow[i] = row;
         koff[i] = row * kvd + 8 * (pch ^ pf_kswz(row));
-        if constexpr (VT) {
-            const uint32_t d = q * 8 + lane / 8;
-            voff[i] = d * p.vt_npad + 8 * ((lane % 8) ^ (d % 8));
-        } else {
-            voff[i] = row * kvd + 8 * (pch ^ pf_vswz(row));
-        }
+        const uint32_t d = q * 8 + lane / 8;  // V^T dim row 8q + l/8, its chunk swizzled by d
+        voff[i] = d * p.vt_npad + 8 * ((lane % 8) ^ (d % 8));
     }
     typedef __attribute__((address_space(3))) void lds_t;
     auto load_block = [&](uint32_t key0, f16* kl) {
         f16* vl = kl + BLK * HD;
         const f16* kb = kcb + (size_t)key0 * kvd;
-        const f16* vb = VT ? vcb + key0 : vcb + (size_t)key0 * kvd;
+        const f16* vb = vcb + key0;
         if (key0 + BLK <= maxlen) {
 #pragma unroll
             for (int i = 0; i < LPW; i++) {
                 const uint32_t q = i * W + w;
                 __builtin_amdgcn_global_load_lds((const void*)(kb + koff[i]), (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(vb + voff[i]), (lds_t*)&vl[q * (VT ? 8 * BLK : RPI * HD)], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(vb + voff[i]), (lds_t*)&vl[q * 8 * BLK], 16, 0, 0);
             }
         } else {
-            // The list's last block: rows past it read the zero page (the packed V^T holds
-            // zeros there already).
 #pragma unroll
             for (int i = 0; i < LPW; i++) {
                 const uint32_t q = i * W + w;
                 const bool ok = key0 + krow[i] < maxlen;
                 const f16* ks = ok ? kb + koff[i] : zp + 8 * (lane % PF_CPR);
-                const f16* vs = (VT || ok) ? vb + voff[i] : zp + 8 * (lane % PF_CPR);
+                const f16* vs = vb + voff[i];  // the packed V^T holds zeros past the list
                 __builtin_amdgcn_global_load_lds((const void*)ks, (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)vs, (lds_t*)&vl[q * (VT ? 8 * BLK : RPI * HD)], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)vs, (lds_t*)&vl[q * 8 * BLK], 16, 0, 0);
             }
         }
     };
@@ -2343,32 +2389,16 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
 #pragma unroll
         for (int c = 0; c < NKC; c++) qb[t][c] = q_scaled(qraw[t][c][0], qraw[t][c][1], p.sc);
 
-    // One block in stage kl: its loads in (own: the wait; everyone's: the barrier, after which
-    // no wave still reads the other stage), the next block's loads out, then scores, mask,
-    // softmax and PV of both tiles.
-    auto iter = [&](uint32_t key0, const f16* kls, f16* nxt) {
+    auto iter = [&](uint32_t key0, const f16* kls, f16* nxt, auto FIRST) {
+        constexpr bool first = decltype(FIRST)::value;
+        // This block in (own loads: the wait; everyone's: the barrier, after which no wave
+        // reads the other stage any more), the next block's loads out into it.
         wait_vm<0>();
         barrier();
         if (key0 + BLK < maxlen) load_block(key0 + BLK, nxt);
-        // Operands are read from LDS one step ahead of the MFMAs that take them: the K tiles of
-        // hd chunk c+1 while chunk c's MFMAs run, the V^T operands of the first key half
-        // while the softmax runs, the second half's while the first half's MFMAs run.
         auto kop = [&](int kt, int c) { return *(const half8*)&kls[kbase[c] + kt * 16 * HD]; };
         const f16* vls = kls + BLK * HD;
-        auto vop = [&](int dt, int kc) -> half8 {
-            if constexpr (VT) {
-                return *(const half8*)&vls[vbase[kc] + dt * 16 * BLK];
-            } else {
-                const uint32_t r = 32 * kc + 4 * g + (n >> 2), ch = 2 * dt + ((n & 3) >> 1), h = n & 1;
-                const half4 lo = lds_tr4(&vls[r * HD + 8 * (ch ^ pf_vswz(r)) + 4 * h]);
-                const uint32_t r2 = r + 16;
-                const half4 hi = lds_tr4(&vls[r2 * HD + 8 * (ch ^ pf_vswz(r2)) + 4 * h]);
-                return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            }
-        };
-        // Scores relative to each slot's running max: the accumulators start at -m (at 0 in
-        // the list's first block, where m is not yet set).
-        const bool first = key0 == 0;
+        auto vop = [&](int dt, int kc) { return *(const half8*)&vls[vbase[kc] + dt * 16 * BLK]; };
         f32x4 sc[NT][4];
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -2376,43 +2406,57 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
 #pragma unroll
             for (int kt = 0; kt < 4; kt++) sc[t][kt] = f32x4{nm, nm, nm, nm};
         }
-        half8 ka[4];
+        // Scores, hd chunks in order; chunk c's K operands were read two chunks earlier.
+        half8 ka[2][4];
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++) ka[kt] = kop(kt, 0);
+        for (int kt = 0; kt < 4; kt++) ka[0][kt] = kop(kt, 0);
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) ka[1][kt] = kop(kt, 1);
+        half8 va[NDT];
 #pragma unroll
         for (int c = 0; c < NKC; c++) {
-            half8 kn[4];
-            if (c + 1 < NKC) {
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++) kn[kt] = kop(kt, c + 1);
-            }
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int t = 0; t < NT; t++) sc[t][kt] = mfma16(ka[kt], qb[t][c], sc[t][kt]);
-            if (c + 1 < NKC) {
+                for (int t = 0; t < NT; t++) sc[t][kt] = mfma16(ka[c & 1][kt], qb[t][c], sc[t][kt]);
+            if (c + 2 < NKC) {
 #pragma unroll
-                for (int kt = 0; kt < 4; kt++) ka[kt] = kn[kt];
+                for (int kt = 0; kt < 4; kt++) ka[c & 1][kt] = kop(kt, c + 2);
+            }
+            if (c == NKC - 2) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) va[dt] = vop(dt, 0);
             }
         }
-        half8 va[NDT];
+        // LDS reads and MFMAs in this order: K chunks 0 and 1; MFMAs of chunk 0; K chunk 2;
+        // MFMAs of chunk 1; K chunk 3; MFMAs of chunk 2; V^T of the first key half; MFMAs of
+        // chunk 3.
+        constexpr int MPC = 4 * NT;  // MFMAs a chunk
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MPC, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MPC, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MPC, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NDT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MPC, 0);
+        // Entries at or past a slot's list length are masked: one test for all tiles (a tile
+        // every slot of which sees the whole block keeps its scores).
+        bool edge = false;
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) va[dt] = vop(dt, 0);
-        half8 pb[NT][2];
+        for (int t = 0; t < NT; t++) edge = edge || key0 + BLK > len[t];
+        if (__any(edge)) {
+            keep_branch();
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (!__all(key0 + BLK <= len[t])) {
-                keep_branch();
+            for (int t = 0; t < NT; t++)
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
                         if (key0 + 16 * kt + 4 * g + i >= len[t]) sc[t][kt][i] = -INFINITY;
-            }
-            float corr;
-            tile_softmax_rel(st[t], sc[t], pb[t], corr, first);
-            rescale(st[t].o, corr);
         }
+        half8 pb[NT][2];
+        tiles_softmax_rel<NDT, NT, first>(st, sc, pb);
         half8 vb[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) vb[dt] = vop(dt, 1);
@@ -2425,11 +2469,14 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
 #pragma unroll
             for (int t = 0; t < NT; t++) st[t].o[dt] = mfma16(vb[dt], pb[t][1], st[t].o[dt]);
     };
-    for (uint32_t key0 = 0;; key0 += 2 * BLK) {
-        iter(key0, ring0, ring1);
-        if (key0 + BLK >= maxlen) break;
-        iter(key0 + BLK, ring1, ring0);
-        if (key0 + 2 * BLK >= maxlen) break;
+    iter(0u, ring0, ring1, std::true_type{});
+    if (BLK < maxlen) {
+        for (uint32_t key0 = BLK;; key0 += 2 * BLK) {
+            iter(key0, ring1, ring0, std::false_type{});
+            if (key0 + BLK >= maxlen) break;
+            iter(key0 + BLK, ring0, ring1, std::false_type{});
+            if (key0 + 2 * BLK >= maxlen) break;
+        }
     }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -2746,31 +2793,22 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
     }
     hipError_t e;
     if (a.kv_type == 1 && a.hd == 128) {
-        // Many rows re-read every V block many times: transpose V once (a pass over V) so
-        // that its operands are plain LDS reads. The result is the same bits either way.
-        // Measured: the pass pays from about 3000 rows (4096 rows of 64/8 heads: 323 against
-        // 330 us a call; 2048 rows of 32/8: 73 against 69 us).
-        const bool use_vt = wide && !sp.split && a.rows >= 3072;
         if (wide && !sp.split) {
             // The wide kernel, two 16-slot tiles a wave, four waves: 128 slots a workgroup as
-            // sp.rb is sized. (One tile a wave, 64 slots a workgroup, measured the same at
-            // 2048 rows: 62.7 against 62.2 us; there the heaviest row block's chain of blocks,
-            // each about 1.9 us of latency, bounds the pass.)
+            // sp.rb is sized, over V transposed once (a pass over V, vt_pack), so that its
+            // operands are plain LDS reads: from 2048 rows the pass pays for itself (2048 rows
+            // of 32/8 heads: 55.8 us of the wide kernel against 61.7 with transposing reads).
             SharedParams lp = sp;
-            if (use_vt) {
-                const uint32_t nb = ceil_div(maxlen, 64);
-                lp.vt_npad = nb * 64;
-                e = ws.reserve_vt((size_t)a.nkv * 128 * lp.vt_npad * 2);
-                if (e != hipSuccess) return e;
-                lp.vt = ws.vt;
-                hipLaunchKernelGGL(vt_pack, dim3(nb, a.nkv), dim3(256), 0, s, (const f16*)a.vc,
-                                   (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, lp.vt_npad);
-                e = hipGetLastError();
-                if (e != hipSuccess) return e;
-                hipExtLaunchKernelGGL((attn_line<true, 2>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, lp);
-            } else {
-                hipExtLaunchKernelGGL((attn_line<false, 2>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, lp);
-            }
+            const uint32_t nb = ceil_div(maxlen, 64);
+            lp.vt_npad = nb * 64;
+            e = ws.reserve_vt((size_t)a.nkv * 128 * lp.vt_npad * 2);
+            if (e != hipSuccess) return e;
+            lp.vt = ws.vt;
+            hipLaunchKernelGGL(vt_pack, dim3(nb, a.nkv), dim3(256), 0, s, (const f16*)a.vc,
+                               (f16*)ws.vt, a.nkv * 128u, (uint32_t)maxlen, lp.vt_npad);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipExtLaunchKernelGGL((attn_line<2>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, lp);
         } else if (wide) {
             hipExtLaunchKernelGGL((attn_prefill<8, false>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else {
