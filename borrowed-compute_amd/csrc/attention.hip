@@ -2176,59 +2176,65 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     }
 }
 
-// The softmax of NT 16-slot tiles of a wave over one 64-entry block, from relative scores,
-// with tile_softmax_rel's arithmetic per slot but the tiles' steps interleaved (each step of
-// every tile before the next step), so that the tiles' dependency chains overlap in one wave,
-// and one uniform branch for all tiles where tile_softmax_rel has one a tile: subtracting a
-// moved max runs for every tile when a slot of any tile moved (a tile none of whose slots
-// moved subtracts 0, exact), and the rescale of O likewise (its slots multiply by 1, exact).
-// FIRST: the list's first block (no running max yet).
+// The softmax of NT 16-slot tiles of a wave over one 64-entry block from relative scores
+// y = s - m (the slot's running max already subtracted by the score MFMAs, whose
+// accumulators start at -m), except in a list's first block (FIRST: y = s, and the block's
+// max becomes m). The running max moves only when a block's relative max passes LAZY; P =
+// 2^y rounded to f16; its block sum is a dot2 chain over the lane's pairs (key tiles in
+// order), then the pairs across lanes l^16 and l^32 (block_step's order); O and l take the
+// factor corr (1 where the max held). The tiles' steps interleave (each step of every tile
+// before the next step), so that their dependency chains overlap in one wave.
 template <int NDT, int NT, bool FIRST>
 __device__ __forceinline__ void tiles_softmax_rel(State<NDT> (&s)[NT], f32x4 (&y)[NT][4], half8 (&pb)[NT][2]) {
-    float my[NT];
+    // The lane's max of each tile (a max is exact in any order).
+    float lm[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        my[t] = fmaxf(fmaxf(y[t][0][0], y[t][0][1]), fmaxf(y[t][0][2], y[t][0][3]));
+        lm[t] = fmaxf(fmaxf(y[t][0][0], y[t][0][1]), fmaxf(y[t][0][2], y[t][0][3]));
 #pragma unroll
         for (int kt = 1; kt < 4; kt++)
-            my[t] = fmaxf(my[t], fmaxf(fmaxf(y[t][kt][0], y[t][kt][1]), fmaxf(y[t][kt][2], y[t][kt][3])));
+            lm[t] = fmaxf(lm[t], fmaxf(fmaxf(y[t][kt][0], y[t][kt][1]), fmaxf(y[t][kt][2], y[t][kt][3])));
     }
-#pragma unroll
-    for (int t = 0; t < NT; t++) my[t] = xmax16(my[t]);
-#pragma unroll
-    for (int t = 0; t < NT; t++) my[t] = xmax32(my[t]);
-    float ms[NT], corr[NT];
+    float corr[NT];
     if constexpr (FIRST) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            ms[t] = (my[t] == -INFINITY) ? 0.0f : my[t];
+            const float my = xmax32(xmax16(lm[t]));
+            const float ms = (my == -INFINITY) ? 0.0f : my;
             corr[t] = 1.0f;  // O and l are still zero
-            s[t].m = my[t];
-        }
-#pragma unroll
-        for (int t = 0; t < NT; t++)
+            s[t].m = my;
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) y[t][kt][i] = y[t][kt][i] - ms[t];
+                for (int i = 0; i < 4; i++) y[t][kt][i] = y[t][kt][i] - ms;
+        }
     } else {
-        bool any = false;
+        // A slot's max moves only if its block max passes LAZY, and then some lane's own max
+        // does: while no lane's does (most blocks of a long list), no slot's max moves, no
+        // score shifts and O and l keep their scale, so the block skips the slots' maxima.
+        bool maybe = false;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            const bool up = my[t] > LAZY;
-            ms[t] = up ? my[t] : 0.0f;
-            corr[t] = up ? exp2_hw(-my[t]) : 1.0f;
-            s[t].m = up ? s[t].m + my[t] : s[t].m;
-            any = any || up;
+            corr[t] = 1.0f;
+            maybe = maybe || lm[t] > LAZY;
         }
-        if (__any(any)) {
+        if (__any(maybe)) {
             keep_branch();
 #pragma unroll
-            for (int t = 0; t < NT; t++)
+            for (int t = 0; t < NT; t++) {
+                const float my = xmax32(xmax16(lm[t]));
+                const bool up = my > LAZY;
+                const float ms = up ? my : 0.0f;
+                corr[t] = up ? exp2_hw(-my) : 1.0f;
+                s[t].m = up ? s[t].m + my : s[t].m;
+                // A slot whose max held subtracts 0 and multiplies by 1: exact.
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) y[t][kt][i] = y[t][kt][i] - ms[t];
+                    for (int i = 0; i < 4; i++) y[t][kt][i] = y[t][kt][i] - ms;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) s[t].o[dt] = s[t].o[dt] * corr[t];
+            }
         }
     }
     uint32_t hp[NT][4][2];
@@ -2258,18 +2264,6 @@ __device__ __forceinline__ void tiles_softmax_rel(State<NDT> (&s)[NT], f32x4 (&y
         for (int kc = 0; kc < 2; kc++)
             pb[t][kc] = __builtin_bit_cast(half8, u32x4{hp[t][2 * kc][0], hp[t][2 * kc][1], hp[t][2 * kc + 1][0],
                                                         hp[t][2 * kc + 1][1]});
-    if constexpr (!FIRST) {
-        bool same = true;
-#pragma unroll
-        for (int t = 0; t < NT; t++) same = same && corr[t] == 1.0f;
-        if (!__all(same)) {
-            keep_branch();
-#pragma unroll
-            for (int t = 0; t < NT; t++)
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++) s[t].o[dt] = s[t].o[dt] * corr[t];
-        }
-    }
 }
 
 // Wide line passes (prefill) on f16 caches at hd 128: every row's list in one online softmax
@@ -2336,36 +2330,48 @@ __global__ __launch_bounds__(256, 2) void attn_line(const SharedParams p) {
     const f16* zp = (const f16*)p.zero;
     const f16* kcb = (const f16*)p.kc + (size_t)kvh * HD;
     const f16* vcb = (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad;
+    // Byte offsets of this wave's load instructions from a block's K rows and V^T columns,
+    // fixed for the loop (32-bit, beside a scalar block base: no 64-bit address arithmetic
+    // a block): K row 4q + l/16 (q = i*W + w), 16-byte chunk l%16 swizzled by the row; V^T
+    // dim row 8q + l/8, chunk l%8 swizzled by the dim row.
+    // Byte offsets of this wave's load instructions from a block's first K row and V^T column,
+    // fixed for the loop: K row 4q + l/16 (q = i*W + w), 16-byte chunk l%16 swizzled by the
+    // row; V^T dim row 8q + l/8, chunk l%8 swizzled by the dim row.
     uint32_t krow[LPW], koff[LPW], voff[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
         const uint32_t q = i * W + w, row = q * RPI + lane / PF_CPR, pch = lane % PF_CPR;
         krow[i] = row;
-        koff[i] = row * kvd + 8 * (pch ^ pf_kswz(row));
-        const uint32_t d = q * 8 + lane / 8;  // V^T dim row 8q + l/8, its chunk swizzled by d
-        voff[i] = d * p.vt_npad + 8 * ((lane % 8) ^ (d % 8));
+        koff[i] = 2 * (row * kvd + 8 * (pch ^ pf_kswz(row)));
+        const uint32_t d = q * 8 + lane / 8;
+        voff[i] = 2 * (d * p.vt_npad + 8 * ((lane % 8) ^ (d % 8)));
     }
     typedef __attribute__((address_space(3))) void lds_t;
     auto load_block = [&](uint32_t key0, f16* kl) {
         f16* vl = kl + BLK * HD;
-        const f16* kb = kcb + (size_t)key0 * kvd;
-        const f16* vb = vcb + key0;
+        const char* kb = (const char*)(kcb + (size_t)key0 * kvd);
+        const char* vb = (const char*)(vcb + key0);
         if (key0 + BLK <= maxlen) {
+            // A whole block: buffer loads from the block's bases (scalar), so the per-lane
+            // offsets stay 32-bit registers fixed for the loop.
+            const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, 0x7fffffff, 0x00020000);
+            const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
             for (int i = 0; i < LPW; i++) {
                 const uint32_t q = i * W + w;
-                __builtin_amdgcn_global_load_lds((const void*)(kb + koff[i]), (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(vb + voff[i]), (lds_t*)&vl[q * 8 * BLK], 16, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_t*)&kl[q * RPI * HD], 16, koff[i], 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_t*)&vl[q * 8 * BLK], 16, voff[i], 0, 0, 0);
             }
         } else {
+            // The list's last block: K rows past it read the zero page (the packed V^T holds
+            // zeros there already).
 #pragma unroll
             for (int i = 0; i < LPW; i++) {
                 const uint32_t q = i * W + w;
                 const bool ok = key0 + krow[i] < maxlen;
-                const f16* ks = ok ? kb + koff[i] : zp + 8 * (lane % PF_CPR);
-                const f16* vs = vb + voff[i];  // the packed V^T holds zeros past the list
-                __builtin_amdgcn_global_load_lds((const void*)ks, (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)vs, (lds_t*)&vl[q * 8 * BLK], 16, 0, 0);
+                const void* ks = ok ? (const void*)(kb + koff[i]) : (const void*)(zp + 8 * (lane % PF_CPR));
+                __builtin_amdgcn_global_load_lds(ks, (lds_t*)&kl[q * RPI * HD], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(vb + voff[i]), (lds_t*)&vl[q * 8 * BLK], 16, 0, 0);
             }
         }
     };
