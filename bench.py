@@ -238,12 +238,14 @@ def bench_multirow(ctx, hip, rows, pos, nh, nkv, hd, reps, n_layer=1, verify=Fal
     return res
 
 
-def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=128, rows=8):
+def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=128, rows=8, fused=False):
     """configs[4]'s speculative decode as configured: 256 steps, each a pass of 8 draft rows
     through the stage's 20 layers, every layer the reference's attention sub-sequence
     (gpu/mod.rs:464-482) for 8 rows: bchip_rope_append (RoPE of q and k, the K/V append at the
-    rows' slots) then bchip_attention over the line; all drafts accepted, so the context grows
-    4096 -> 6136 by 8 a step. Timed as one region: the stream time of all 256 x 20 layer-steps."""
+    rows' slots) then bchip_attention over the line, or (fused) the one call that stands for
+    both, bchip_rope_append_attention_rows (the same bits); all drafts accepted, so the context
+    grows 4096 -> 6136 by 8 a step. Timed as one region: the stream time of all 256 x 20
+    layer-steps."""
     kvd = nkv * hd
     cap = ctx0 + steps * rows
     kcs, vcs = [], []
@@ -267,6 +269,10 @@ def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=12
             q = qkv.ptr + layer * per * 4
             k = q + rows * nh * hd * 4
             v = k + rows * kvd * 4
+            if fused:
+                ctx.rope_append_attention_rows(q, k, v, kcs[layer], vcs[layer], bchip.F16, inv, pos.ptr + 4 * s * rows,
+                                               rows, nh, nkv, hd, hd, False, base, scale, out)
+                continue
             ctx.rope_append(q, k, v, kcs[layer], vcs[layer], bchip.F16, inv, pos.ptr + 4 * s * rows, rows, nh, nkv,
                             hd, hd, False, base)
             ctx.attention(q, kcs[layer], vcs[layer], bchip.F16, out, None, False, rows, nh, nkv, hd, base, scale)
@@ -282,7 +288,8 @@ def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=12
     kv_bytes = sum(2.0 * (ctx0 + (s + 1) * rows) * kvd * 2 for s in range(steps)) * n_layer
     layer_steps = steps * n_layer
     return {"steps": steps, "rows": rows, "ctx": [ctx0, ctx0 + steps * rows], "layers": n_layer,
-            "calls_per_layer_step": "bchip_rope_append + bchip_attention", "total_ms": total_ms,
+            "calls_per_layer_step": "bchip_rope_append_attention_rows" if fused else "bchip_rope_append + bchip_attention",
+            "total_ms": total_ms,
             "us_per_layer_step": total_ms * 1e3 / layer_steps,
             "tokens_per_s": rows * steps / (total_ms * 1e-3),
             "kv_GBps": kv_bytes / (total_ms * 1e-3) / 1e9, "kv_hbm_frac": kv_bytes / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -603,6 +610,9 @@ def main():
             log("Llama-3-70B share: 256 verify steps of 8 rows, 20 layers, rope_append + attention a layer-step")
             extra["verify_loop_70b_256"] = bench_verify_loop(ctx)
             log(json.dumps(extra["verify_loop_70b_256"]))
+            log("the same loop through the single call for the layer's rotations, appends and attention")
+            extra["verify_loop_70b_256_fused"] = bench_verify_loop(ctx, fused=True)
+            log(json.dumps(extra["verify_loop_70b_256_fused"]))
         if "f32" in want:
             # The drop-in default: an unmodified binding passes the reference's f32 cache
             # (bchip_rope_append_attention with BCHIP_F32: rope_append, then attn_f32).

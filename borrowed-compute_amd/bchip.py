@@ -80,6 +80,8 @@ def lib() -> ctypes.CDLL:
         "bchip_rope_append_attention": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32, P], i32),
         "bchip_rope_append_attention_noalloc": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, f32,
                                                  P], i32),
+        "bchip_rope_append_attention_rows": ([P, P, P, P, P, P, u32, P, P, u32, u32, u32, u32, u32, u32, u32, f32,
+                                              P], i32),
         "bchip_attention_ragged": ([P, P, P, P, u32, P, P, P, u32, u32, u32, u32, f32], i32),
         "bchip_rope_append_ragged": ([P, P, P, P, P, P, u32, P, P, P, P, u32, u32, u32, u32, u32, u32], i32),
         "bchip_rope_append_attention_ragged": ([P, P, P, P, P, P, u32, P, P, P, P, u32, u32, u32, u32, u32, u32, f32,
@@ -232,6 +234,13 @@ class Ctx:
         check(lib().bchip_rope_append_attention(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc), kv_type,
                                                 _ptr(inv_freq), _ptr(positions), nh, nkv, hd, rope_dim, int(neox),
                                                 pos, scale, _ptr(out)))
+
+    def rope_append_attention_rows(self, q, k, v, kc, vc, kv_type, inv_freq, positions, rows, nh, nkv, hd, rope_dim,
+                                   neox, pos, scale, out) -> None:
+        """rope_append of `rows` rows at slot pos, then attention of those rows at pos, in one call."""
+        check(lib().bchip_rope_append_attention_rows(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(kc), _ptr(vc), kv_type,
+                                                     _ptr(inv_freq), _ptr(positions), rows, nh, nkv, hd, rope_dim,
+                                                     int(neox), pos, scale, _ptr(out)))
 
     def rope_append_attention_noalloc(self, q, k, v, kc, vc, kv_type, inv_freq, positions, nh, nkv, hd, rope_dim,
                                       neox, pos, scale, out) -> None:

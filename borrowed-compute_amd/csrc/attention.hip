@@ -1645,6 +1645,8 @@ __device__ __forceinline__ void tile_softmax(State<NDT>& s, const f32x4 (&x)[4],
 // as n * sum(x^2) == sum(x)^2 exactly when every x is the same), the second arrivals, and the
 // departures; the last workgroup to leave clears them for the next call.
 constexpr uint32_t GFOLD_MAX_CHUNKS = 32;
+// Rows a fused multi-row pass takes (one row block: 64 slots of at least 4 heads a KV head).
+constexpr uint32_t FUSE_ROWS = 16;
 // A wait takes at most SharedParams::gspins polls (2^16 unless a test lowers it), each a
 // counter read and ~128 clocks of sleep.
 enum : uint32_t { GS_ARRIVE = 0, GS_ARRIVE2 = 2, GS_LEAVE = 3 };
@@ -1851,7 +1853,7 @@ __device__ __forceinline__ void group_fold_slots(const SharedParams& p, uint32_t
 template <int N>
 using ic = std::integral_constant<int, N>;
 
-template <int W, bool VT>
+template <int W, bool VT, bool FUSE>
 __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     constexpr int HD = 128;
     constexpr int NKC = HD / 32, NDT = HD / 16;
@@ -1867,6 +1869,13 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     __shared__ __attribute__((aligned(16))) f16 ring2[SZ];
     // Each wave's Q tile as loaded: 2 * NKC rows of 64 lanes x 4 floats.
     __shared__ __attribute__((aligned(16))) float qlds[W][2 * NKC * 256];
+    // FUSE: the rotations' sines and cosines, row rl of the workgroup and pair pp at
+    // rsc[64 rl + pp] (hd 128: 64 pairs); after the blocks, the group fold's flag word.
+    __shared__ float2 rsc[FUSE ? FUSE_ROWS * 64 : 1];
+    // FUSE: the launch's new rows of this KV head as the cache holds them, K rotated: [row][hd].
+    __shared__ __attribute__((aligned(16))) f16 nrow[FUSE ? 2 : 1][FUSE ? FUSE_ROWS * HD : 8];
+    // FUSE: each wave's copy of the rotation frequencies (pair pp), loaded direct to LDS.
+    __shared__ __attribute__((aligned(16))) float sfreq[FUSE ? W : 1][64];
     auto ring = [&](auto S) -> f16* {
         if constexpr (decltype(S)::value == 0) return ring0;
         else if constexpr (decltype(S)::value == 1) return ring1;
@@ -1916,6 +1925,13 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         // LDS object, so the conversion below waits for Q alone, not for the blocks issued
         // after it (loads into registers would be counted as the last ones issued).
         typedef __attribute__((address_space(3))) void lds_q_t;
+        if constexpr (FUSE) {
+            // FUSE: first this wave's copy of the rotation frequencies (pair pp = lane; pairs
+            // past rope_dim / 2 read the zero page), so that the table can go before Q lands.
+            __builtin_amdgcn_global_load_lds(
+                (const void*)((uint32_t)lane < p.rope_dim / 2 ? p.inv_freq + lane : (const float*)p.zero),
+                (lds_q_t*)&sfreq[w][0], 4, 0, 0);
+        }
 #pragma unroll
         for (int c = 0; c < NKC; c++) {
             const float* src = valid ? qrow + 32 * c + 8 * g : qrow;
@@ -1935,6 +1951,29 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     // Per-lane element offsets of this wave's load instructions, fixed for the loop: K row
     // 4q + l/16 (q = i*W + w), 16-byte chunk l%16 swizzled by the row; V^T dim row 8q + l/8,
     // chunk l%8 swizzled by the dim row (VT), else V rows as K.
+    // FUSE: the small loads go direct to LDS before the blocks' (a wave's loads complete in
+    // issue order, and loads into registers would make the compiler wait for every load in
+    // flight before their first use): the frequencies (above, before Q), and, for a chunk that
+    // holds new rows, the rows of k and v of this KV head (f32, [row][hd]) into the third ring
+    // stage, which the blocks reach only after the prologue. Rows past the launch's read the
+    // zero page.
+    typedef __attribute__((address_space(3))) void lds_f_t;
+    const bool has_new = FUSE && kb1 > p.pos;
+    float* raw = (float*)ring2;  // FUSE: k rows at raw[r * HD], v rows at raw[FUSE_ROWS * HD + r * HD]
+    if constexpr (FUSE) {
+        const float* zf = (const float*)p.zero;
+        if (has_new) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint32_t c = (2 * w + i) * 64 + lane, r = c / 32, d = 4 * (c % 32);  // 16-byte pieces
+                const bool ok = r < p.rows;
+                const size_t at = ((size_t)r * p.nkv + kvh) * HD + d;
+                __builtin_amdgcn_global_load_lds((const void*)(ok ? p.knew + at : zf), (lds_f_t*)&raw[(2 * w + i) * 256], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(ok ? p.vnew + at : zf),
+                                                 (lds_f_t*)&raw[FUSE_ROWS * HD + (2 * w + i) * 256], 16, 0, 0);
+            }
+        }
+    }
     const f16* zp = (const f16*)p.zero;
     const f16* kcb = (const f16*)p.kc + (size_t)kvh * HD;
     const f16* vcb = VT ? (const f16*)p.vt + (size_t)kvh * HD * p.vt_npad : (const f16*)p.vc + (size_t)kvh * HD;
@@ -2015,26 +2054,198 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
     // loads as younger than Q's).
     load_block(kb0, ic<0>{});
     load_block(kb0 + BLK, ic<1>{});
-    if (kb0 + BLK < kb1)
+    // Blocks now in flight (their load instructions, this wave).
+    const int inflight = kb0 + BLK < kb1 ? 2 : kb0 < kb1 ? 1 : 0;
+    if constexpr (FUSE) {
+        // The frequencies in (the wait leaves Q, the new rows and the blocks in flight: they went
+        // out after them, in that order), then
+        // the table of the rotations' sines and cosines, row rl of the workgroup and pair pp at
+        // rsc[64 rl + pp], wave w taking rows w, w + W, ...
+        constexpr int NQ = 2 * NKC, NR = 4;  // Q's and the new rows' load instructions, this wave
+        if (has_new) {
+            if (inflight == 2) wait_vm<NQ + NR + 2 * LPB>();
+            else if (inflight == 1) wait_vm<NQ + NR + LPB>();
+            else wait_vm<NQ + NR>();
+        } else {
+            if (inflight == 2) wait_vm<NQ + 2 * LPB>();
+            else if (inflight == 1) wait_vm<NQ + LPB>();
+            else wait_vm<NQ>();
+        }
+        // The frequency read is written out: the compiler would wait for every load in flight
+        // before an LDS read it cannot tell apart from their destinations.
+        float fr;
+        {
+            const uint32_t fa =
+                (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&sfreq[w][lane];
+            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(fr) : "v"(fa) : "memory");
+        }
+        // Row rl of the workgroup's rows (uniform in the wave: its position is a scalar load).
+        const auto* pos4 = (const __attribute__((address_space(4))) uint32_t*)p.positions;
+#pragma unroll 1
+        for (uint32_t rl = (uint32_t)w; rl < p.rb; rl += W) {
+            const uint32_t r = r0 + rl;
+            const float th = (float)pos4[r < p.rows ? r : 0u] * fr;
+            float sn, cs;
+            sincosf(th, &sn, &cs);
+            rsc[rl * 64 + lane] = float2{sn, cs};
+        }
+    }
+    // Q in (and the new rows), the blocks still in flight.
+    if (inflight == 2)
         wait_vm<2 * LPB>();
-    else if (kb0 < kb1)
+    else if (inflight == 1)
         wait_vm<LPB>();
     else
         wait_vm<0>();
+    if constexpr (FUSE) {
+        // Everyone's table and new rows in (the barrier; no wait for the blocks in flight).
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        barrier();
+        // The new rows as the cache will hold them, K rotated by the table's row (pair (a, b):
+        // neox (pp, pp + hr), else (2pp, 2pp + 1); y0 = x_a c - x_b s, y1 = x_a s + x_b c, as
+        // k_rope_append), into nrow: thread tid takes row tid / 16, dims 8 (tid % 16) .. +7.
+        if (has_new) {
+            const uint32_t hr = p.rope_dim / 2, r = tid / 16, d0 = 8 * (tid % 16);
+            if (r < p.rows) {
+                const float* kx = raw + r * HD;
+                const float* vx = raw + FUSE_ROWS * HD + r * HD;
+                half8 kh, vh;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const uint32_t d = d0 + j;
+                    float y = kx[d];
+                    if (d < p.rope_dim) {
+                        const bool first = p.neox ? d < hr : (d & 1u) == 0u;
+                        const uint32_t e = p.neox ? (first ? d + hr : d - hr) : (d ^ 1u);
+                        const uint32_t pp = p.neox ? (first ? d : e) : d / 2;
+                        const float2 t = rsc[(r - r0) * 64 + pp];
+                        float y0, y1;
+                        if (first)
+                            rotate_sc(kx[d], kx[e], t.x, t.y, y0, y1);
+                        else
+                            rotate_sc(kx[e], kx[d], t.x, t.y, y0, y1);
+                        y = first ? y0 : y1;
+                    }
+                    kh[j] = to_kv<f16>(y);
+                    vh[j] = to_kv<f16>(vx[d]);
+                }
+                *(half8*)&nrow[0][r * HD + d0] = kh;
+                *(half8*)&nrow[1][r * HD + d0] = vh;
+            }
+        }
+        // nrow in before any block reads it, and every read of the staged rows in the third
+        // stage done before its block's loads.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        barrier();
+    }
     {
         const uint32_t qa = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&qlds[w][4 * lane];
+        // FUSE: the sines and cosines of this lane's pairs (slot n's row) come in with Q, four
+        // pairs a read: adjacent pairs 16 (k / 2) + 4 (lane / 16) + 0..3 (k = 0, 2, 4, 6), neox
+        // pairs 32 (k / 2) + 8 (lane / 16) + 4 (k % 2) + 0..3 (k < 4; rope_dim 64 uses the
+        // first two). The table's reads are written out too, and listed as operands of Q's
+        // reads, whose wait covers them.
+        f32x4 t4[FUSE ? 8 : 1];
+        const uint32_t db = 8u * (uint32_t)(lane / 16);
         f32x4 qv[2 * NKC];
-        asm volatile(
-            "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:1024\n\t"
-            "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %8 offset:3072\n\t"
-            "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %8 offset:5120\n\t"
-            "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %8 offset:7168\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(qv[0]), "=&v"(qv[1]), "=&v"(qv[2]), "=&v"(qv[3]), "=&v"(qv[4]), "=&v"(qv[5]), "=&v"(qv[6]),
-              "=&v"(qv[7])
-            : "v"(qa)
-            : "memory");
+#define BCHIP_Q_READS(A)                                                              \
+    "ds_read_b128 %0, %" #A "\n\tds_read_b128 %1, %" #A " offset:1024\n\t"            \
+    "ds_read_b128 %2, %" #A " offset:2048\n\tds_read_b128 %3, %" #A " offset:3072\n\t" \
+    "ds_read_b128 %4, %" #A " offset:4096\n\tds_read_b128 %5, %" #A " offset:5120\n\t" \
+    "ds_read_b128 %6, %" #A " offset:6144\n\tds_read_b128 %7, %" #A " offset:7168\n\t"
+        if constexpr (FUSE) {
+            const uint32_t tb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float2*)&rsc[0] +
+                                ((16u * w + n) % p.rb) * 512u;
+            if (!p.neox)
+                asm volatile(
+                    "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
+                    "ds_read_b128 %2, %8 offset:128\n\tds_read_b128 %3, %8 offset:144\n\t"
+                    "ds_read_b128 %4, %8 offset:256\n\tds_read_b128 %5, %8 offset:272\n\t"
+                    "ds_read_b128 %6, %8 offset:384\n\tds_read_b128 %7, %8 offset:400"
+                    : "=&v"(t4[0]), "=&v"(t4[1]), "=&v"(t4[2]), "=&v"(t4[3]), "=&v"(t4[4]), "=&v"(t4[5]),
+                      "=&v"(t4[6]), "=&v"(t4[7])
+                    : "v"(tb + 4u * db)
+                    : "memory");
+            else
+                asm volatile(
+                    "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
+                    "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
+                    "ds_read_b128 %4, %8 offset:256\n\tds_read_b128 %5, %8 offset:272\n\t"
+                    "ds_read_b128 %6, %8 offset:288\n\tds_read_b128 %7, %8 offset:304"
+                    : "=&v"(t4[0]), "=&v"(t4[1]), "=&v"(t4[2]), "=&v"(t4[3]), "=&v"(t4[4]), "=&v"(t4[5]),
+                      "=&v"(t4[6]), "=&v"(t4[7])
+                    : "v"(tb + 8u * db)
+                    : "memory");
+            asm volatile(BCHIP_Q_READS(16) "s_waitcnt lgkmcnt(0)"
+                         : "=&v"(qv[0]), "=&v"(qv[1]), "=&v"(qv[2]), "=&v"(qv[3]), "=&v"(qv[4]), "=&v"(qv[5]),
+                           "=&v"(qv[6]), "=&v"(qv[7]), "+v"(t4[0]), "+v"(t4[1]), "+v"(t4[2]), "+v"(t4[3]),
+                           "+v"(t4[4]), "+v"(t4[5]), "+v"(t4[6]), "+v"(t4[7])
+                         : "v"(qa)
+                         : "memory");
+        } else {
+            asm volatile(BCHIP_Q_READS(8) "s_waitcnt lgkmcnt(0)"
+                         : "=&v"(qv[0]), "=&v"(qv[1]), "=&v"(qv[2]), "=&v"(qv[3]), "=&v"(qv[4]), "=&v"(qv[5]),
+                           "=&v"(qv[6]), "=&v"(qv[7])
+                         : "v"(qa)
+                         : "memory");
+        }
+#undef BCHIP_Q_READS
         static_assert(NKC == 4, "eight 1 KB rows of Q a wave");
+        if constexpr (FUSE) {
+            // Q rotated in registers as k_rope_append rotates it (the same expressions, so the
+            // same bits): lane holds slot n's dims 32 (k / 2) + 8 (lane / 16) + 4 (k % 2) + j in
+            // qv[k][j], so an adjacent pair is two elements of one register and a neox pair
+            // (d, d + rope_dim / 2, rope_dim 64 or 128: the launch checks) the same element of
+            // qv[k] and qv[k + rope_dim / 32]. Every rotation is computed, kept where the pair
+            // is rotated (no branches on the lane's dims).
+            if (!p.neox) {
+#pragma unroll
+                for (int k = 0; k < 2 * NKC; k++)
+#pragma unroll
+                    for (int j = 0; j < 4; j += 2) {
+                        const uint32_t d = 32u * (k / 2) + db + 4u * (k % 2) + j;
+                        const f32x4& t2 = t4[2 * (k / 2) + k % 2];  // pairs 2 (k % 2) + 0, 1
+                        const float2 t = j == 0 ? float2{t2[0], t2[1]} : float2{t2[2], t2[3]};
+                        float y0, y1;
+                        rotate_sc(qv[k][j], qv[k][j + 1], t.x, t.y, y0, y1);
+                        const bool rot = d < p.rope_dim;
+                        qv[k][j] = rot ? y0 : qv[k][j];
+                        qv[k][j + 1] = rot ? y1 : qv[k][j + 1];
+                    }
+            } else {
+                auto rot = [&](auto KH) {
+                    constexpr int kh = decltype(KH)::value;
+#pragma unroll
+                    for (int k = 0; k < kh; k++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const f32x4& t2 = t4[2 * k + j / 2];
+                            const float2 t = j % 2 == 0 ? float2{t2[0], t2[1]} : float2{t2[2], t2[3]};
+                            float y0, y1;
+                            rotate_sc(qv[k][j], qv[k + kh][j], t.x, t.y, y0, y1);
+                            qv[k][j] = y0;
+                            qv[k + kh][j] = y1;
+                        }
+                };
+                if (p.rope_dim == 128)
+                    rot(ic<4>{});
+                else
+                    rot(ic<2>{});
+            }
+            // The workgroup that writes the rotated Q back keeps it in its LDS rows until then
+            // (written out, like the read).
+            if (cs_idx == 0) {
+                asm volatile(
+                    "ds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:1024\n\t"
+                    "ds_write_b128 %0, %3 offset:2048\n\tds_write_b128 %0, %4 offset:3072\n\t"
+                    "ds_write_b128 %0, %5 offset:4096\n\tds_write_b128 %0, %6 offset:5120\n\t"
+                    "ds_write_b128 %0, %7 offset:6144\n\tds_write_b128 %0, %8 offset:7168"
+                    :
+                    : "v"(qa), "v"(qv[0]), "v"(qv[1]), "v"(qv[2]), "v"(qv[3]), "v"(qv[4]), "v"(qv[5]), "v"(qv[6]),
+                      "v"(qv[7])
+                    : "memory");
+            }
+        }
 #pragma unroll
         for (int c = 0; c < NKC; c++) {
             const f32x4 a = qv[2 * c], b = qv[2 * c + 1];
@@ -2042,6 +2253,27 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         }
     }
 
+    // FUSE: this wave's rows of the block at key0 that are new (slot pos + r for row r of the
+    // launch): K dims 8 (lane % 16 ^ swizzle) .. +7 and V's dims of the V load pattern, from
+    // the staged rows (K rotated, both rounded to the cache type), into the stage (over what the
+    // block's loads brought for those rows) and into the caches.
+    auto new_rows = [&](uint32_t key0, f16* kl) {
+        f16* vl = kl + BLK * HD;
+#pragma unroll
+        for (int i = 0; i < LPW; i++) {
+            const uint32_t q = i * W + w, row = q * RPI + lane / PF_CPR, pch = lane % PF_CPR;
+            const uint32_t key = key0 + row;
+            if (key < p.pos || key >= kb1) continue;
+            const uint32_t r = key - p.pos;
+            const uint32_t dk = 8 * (pch ^ pf_kswz(row)), dv = 8 * (pch ^ pf_vswz(row));
+            const half8 kh = *(const half8*)&nrow[0][r * HD + dk];
+            const half8 vh = *(const half8*)&nrow[1][r * HD + dv];
+            *(half8*)&kl[q * RPI * HD + 8 * lane] = kh;
+            *(half8*)&vl[q * RPI * HD + 8 * lane] = vh;
+            *(half8*)((f16*)p.kc + (size_t)key * kvd + (size_t)kvh * HD + dk) = kh;
+            *(half8*)((f16*)p.vc + (size_t)key * kvd + (size_t)kvh * HD + dv) = vh;
+        }
+    };
     // One block in stage S: scores, mask, softmax, PV.
     auto iter = [&](uint32_t key0, auto S) -> bool {
         constexpr int s0 = decltype(S)::value;
@@ -2053,6 +2285,15 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
             wait_vm<LPB>();
         else
             wait_vm<0>();
+        if constexpr (FUSE) {
+            // The launch's new rows in this block: each wave writes the rows its own loads
+            // brought (they have landed), K rotated and V as the cache holds them, into the
+            // stage and into the caches.
+            if (key1 > p.pos) {
+                new_rows(key0, ring(S));
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the rows are in the stage
+            }
+        }
         barrier();
         load_block(key0 + (STAGES - 1) * BLK, ic<(s0 + STAGES - 1) % STAGES>{});
         // S^T = K . Q^T: four key tiles, hd chunks accumulated in order.
@@ -2153,13 +2394,24 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(const SharedParams p) {
         // Group fold. Q's LDS rows are free for the flag word: each wave read its own rows
         // before its first block.
         GroupSync gsync{p.gcnt + (size_t)grp * GROUP_STRIDE, p.nchunk, p.gspins, p.gspread, 0u};
-        uint32_t& flag = *(uint32_t*)&qlds[0][0];
+        uint32_t& flag = FUSE ? *(uint32_t*)&rsc[0] : *(uint32_t*)&qlds[0][0];
         uint32_t mode = group_arrive(gsync, p.gerr, flag);
         if (mode == GF_SPREAD) {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) store_wt4(po + 16 * dt + 4 * g, cs.o[dt]);
             if (g == 0) store_wt2(p.part_ml + at * 2, cs.m, cs.l);
             mode = group_second(gsync, p.gerr, flag);
+        }
+        if constexpr (FUSE) {
+            // Every workgroup of the group has read its q: the first one leaves it rotated.
+            if (cs_idx == 0 && valid && mode != GF_TIMEOUT) {
+                float* dst = p.qw + ((size_t)orow * p.nh + ohead) * HD;
+#pragma unroll
+                for (int c = 0; c < NKC; c++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        *(float4*)(dst + 32 * c + 8 * g + 4 * h) = *(const float4*)&qlds[w][(2 * c + h) * 256 + 4 * lane];
+            }
         }
         // The ring's first stage is free: every wave is past its last block.
         group_fold_slots<16 * W>(p, grp, cs_idx, rbi, kvh, mode != GF_TIMEOUT, (float4*)ring0);
@@ -2751,7 +3003,15 @@ hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitem
     return e;
 }
 
-hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
+static hipError_t shared_plan(const AttnCall& a, Workspace& ws, hipStream_t s, const RopeArgs* rope);
+
+hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) { return shared_plan(a, ws, s, nullptr); }
+
+hipError_t shared_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s) {
+    return shared_plan(a, ws, s, &r);
+}
+
+static hipError_t shared_plan(const AttnCall& a, Workspace& ws, hipStream_t s, const RopeArgs* rope) {
     SharedParams sp{};
     sp.zero = ws.zero;
     sp.q = a.q;
@@ -2798,6 +3058,24 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
         sp.gspins = ws.group_spins;
     }
     hipError_t e;
+    if (rope) {
+        // The fused form: one row block (every row's q rotated by the workgroups that read it),
+        // the split pass's group fold (the rotated q is written once every workgroup of a group
+        // has read it), the table of one row block's rotations, neox pairs a multiple of 32
+        // dims apart (q is rotated in the registers it is read into).
+        if (!(gfold && !wide && a.kv_type == 1 && a.hd == 128 && sp.nrb == 1 && sp.rb <= FUSE_ROWS &&
+              rope->rope_dim <= a.hd && (!rope->neox || rope->rope_dim == 64 || rope->rope_dim == 128)))
+            return hipErrorNotSupported;
+        sp.knew = rope->k;
+        sp.vnew = rope->v;
+        sp.inv_freq = rope->inv_freq;
+        sp.positions = rope->positions;
+        sp.rope_dim = rope->rope_dim;
+        sp.neox = rope->neox;
+        sp.qw = rope->q;
+        hipExtLaunchKernelGGL((attn_prefill<4, false, true>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
+        return hipGetLastError();
+    }
     if (a.kv_type == 1 && a.hd == 128) {
         if (wide && !sp.split) {
             // The wide kernel, two 16-slot tiles a wave, four waves: 128 slots a workgroup as
@@ -2816,9 +3094,9 @@ hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s) {
             if (e != hipSuccess) return e;
             hipExtLaunchKernelGGL((attn_line<2>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, lp);
         } else if (wide) {
-            hipExtLaunchKernelGGL((attn_prefill<8, false>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
+            hipExtLaunchKernelGGL((attn_prefill<8, false, false>), dim3(blocks), dim3(512), 0, s, a.ev_before, a.ev_after, 0, sp);
         } else {
-            hipExtLaunchKernelGGL((attn_prefill<4, false>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
+            hipExtLaunchKernelGGL((attn_prefill<4, false, false>), dim3(blocks), dim3(256), 0, s, a.ev_before, a.ev_after, 0, sp);
         }
         e = hipGetLastError();
     } else if (a.kv_type == 1) {

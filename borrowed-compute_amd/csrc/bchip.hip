@@ -52,6 +52,11 @@ struct bchip_ctx {
         a.ev_after = arm_after;
         arm_before = arm_after = nullptr;
     }
+    // Hands an arming taken by a call that launched nothing back for the call after it.
+    void restore_marks(const bchip::AttnCall& a) {
+        arm_before = a.ev_before;
+        arm_after = a.ev_after;
+    }
 };
 
 namespace {
@@ -664,6 +669,47 @@ int bchip_attention(bchip_ctx* c, const float* q, const void* kc, const void* vc
     }
     HIP_TRY(e, "attention");
     return BCHIP_OK;
+}
+
+int bchip_rope_append_attention_rows(bchip_ctx* c, float* q, const float* k, const float* v, void* kc, void* vc,
+                                     uint32_t kv_type, const float* inv_freq, const uint32_t* positions,
+                                     uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim,
+                                     uint32_t neox, uint32_t pos, float scale, float* out) {
+    CHECK(enter(c));
+    if (rows == 0) return BCHIP_OK;
+    if (!q || !k || !v || !kc || !vc || !inv_freq || !positions || !out) return fail(BCHIP_E_ARG, "null pointer");
+    if (kv_type > 1) return fail(BCHIP_E_ARG, "element type %u", kv_type);
+    CHECK(check_heads(nh, nkv, hd));
+    if (rope_dim % 2 || rope_dim > hd) return fail(BCHIP_E_ARG, "rope_dim %u for head_dim %u", rope_dim, hd);
+    if (!aligned16(q) || !aligned16(out) || !aligned16(kc) || !aligned16(vc))
+        return fail(BCHIP_E_ARG, "q, out and the caches must be 16-byte aligned");
+    if ((uint64_t)pos + rows > 0xffffffffull) return fail(BCHIP_E_ARG, "position past 2^32");
+    const uint64_t kvd = (uint64_t)nkv * hd, slots = (uint64_t)pos + rows;
+    CHECK(check_span(c, q, sat_mul(sat_mul(rows, nh), (uint64_t)hd * 4), "q"));
+    CHECK(check_span(c, out, sat_mul(sat_mul(rows, nh), (uint64_t)hd * 4), "out"));
+    CHECK(check_span(c, k, sat_mul(rows, kvd * 4), "k"));
+    CHECK(check_span(c, v, sat_mul(rows, kvd * 4), "v"));
+    CHECK(check_span(c, kc, sat_mul(slots, kvd * esize(kv_type)), "kc"));
+    CHECK(check_span(c, vc, sat_mul(slots, kvd * esize(kv_type)), "vc"));
+    CHECK(check_span(c, positions, (uint64_t)rows * 4, "positions"));
+    CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
+    if (kv_type == BCHIP_F16 && rows > 1) {
+        const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
+        AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, rows, nh, nkv, hd, pos, scale, limit};
+        const RopeArgs r{q, k, v, inv_freq, positions, rope_dim, neox};
+        c->take_marks(a);
+        const hipError_t e = shared_attention_fused(a, r, c->ws, c->stream);
+        if (e != hipErrorNotSupported) {
+            HIP_TRY(e, "rope_append_attention_rows");
+            return BCHIP_OK;
+        }
+        c->restore_marks(a);
+    }
+    // Shapes the fused launch does not take: the two calls.
+    HIP_TRY(rope_append_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, rows, nh, nkv, hd, rope_dim, neox, pos,
+                               c->stream),
+            "rope_append");
+    return bchip_attention(c, q, kc, vc, kv_type, out, nullptr, 0, rows, nh, nkv, hd, pos, scale);
 }
 
 // bchip_rope_append_attention on workspace ws; with a fixed workspace (the no-allocation

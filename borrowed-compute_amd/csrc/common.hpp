@@ -168,6 +168,16 @@ struct SharedParams {
     uint32_t xmap;  // split launches: blocks 8 apart take one group's chunks (one XCD each)
     uint32_t gspread;  // group fold: take the spread path whatever the XCDs (tests)
     uint32_t gspins;   // group fold: polls a wait may take
+    // Multi-row passes fused with RoPE and the K/V append (attn_prefill's FUSE form): q is
+    // unrotated on entry and left rotated in qw; row r's new k and v (f32 [rows][nkv][hd])
+    // go, k rotated, into the caches at slot pos + r, and the launch takes them from LDS for
+    // those slots. positions: the rows' rotation positions.
+    const float* knew;
+    const float* vnew;
+    const float* inv_freq;
+    const uint32_t* positions;
+    uint32_t rope_dim, neox;
+    float* qw;
 };
 
 struct CombineParams {

@@ -96,6 +96,11 @@ size_t row_state_slots(uint64_t len, uint32_t nkv);
 hipError_t direct_attention(const AttnCall& a, const Item* items, uint32_t nitems,
                             Workspace& ws, hipStream_t s);
 hipError_t shared_attention(const AttnCall& a, Workspace& ws, hipStream_t s);
+// A line of rows (verify) with RoPE and the K/V append of its rows (slots pos + r) in the
+// same launch: the bits of rope_append_launch then shared_attention. hipErrorNotSupported
+// (nothing launched) where the plan is not a split pass folded in its launch of f16 hd-128
+// caches of at most FUSE_ROWS rows: the caller then makes the two calls.
+hipError_t shared_attention_fused(const AttnCall& a, const RopeArgs& r, Workspace& ws, hipStream_t s);
 // The left fold of chunk states (attn_combine) over `groups` groups of cp.
 hipError_t combine_launch(CombineParams& cp, uint32_t groups, uint32_t hd, hipStream_t s);
 // Every call on an f32 cache (lines, trees, one row): f32 arithmetic throughout

@@ -161,6 +161,22 @@ int bchip_rope_append_attention(bchip_ctx* ctx, float* q, const float* k, const 
                                 uint32_t nkv, uint32_t hd, uint32_t rope_dim, uint32_t neox, uint32_t pos,
                                 float scale, float* out);
 
+/* One layer of a multi-row pass (a speculative verify step, llm.rs:655-667; a chain of
+ * draft rows) as a single call: bchip_rope_append with slot0 = pos, then bchip_attention
+ * (tree = 0) of the same rows at pos, with the same results bit for bit (out; q left
+ * rotated; rows r of k and v in slots pos + r of kc and vc). It is the peephole over the
+ * commands k_rope(q), k_rope(k), k_copy(k), k_copy(v), k_attention that Layers::forward
+ * queues per layer for a pass of several rows (gpu/mod.rs:464-482). One launch does the
+ * rotations, the appends and the attention (its workgroups take the new rows from LDS) for
+ * f16 caches at head_dim 128, at most 16 rows with rows x (nh / nkv) <= 64, a line longer
+ * than one 192-slot chunk whose split launch fits the device's CUs at once, and neox pairs
+ * only at rope_dim 64 or 128; other shapes run as the two calls.
+ * positions: device u32 [rows]. */
+int bchip_rope_append_attention_rows(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
+                                     uint32_t kv_type, const float* inv_freq, const uint32_t* positions,
+                                     uint32_t rows, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t rope_dim,
+                                     uint32_t neox, uint32_t pos, float scale, float* out);
+
 /* bchip_rope_append_attention that allocates nothing. It has no counterpart in the
  * reference; it is for callers that cannot allocate device memory mid-run (code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation). Same arguments and
