@@ -8,6 +8,7 @@ oracle gate. The cases cover the fused launch (a split pass folded in its launch
 verify at 4096 and 6136 slots, new rows crossing a block and a chunk boundary, adjacent and
 neox pairs, partial rotary dims) and the shapes that run as the two calls."""
 import math
+import os
 
 import numpy as np
 import pytest
@@ -118,3 +119,54 @@ def test_rows_step_repeats_bit_for_bit(ctx):
     np.testing.assert_array_equal(outs[0], outs[2])
     for b in (ib, pb, kb, vb):
         b.free()
+
+
+def _ctx_with(env):
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return bchip.Ctx(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+def _step(c, fused, q, k, v, kc0, vc0, inv, positions, rows, nh, nkv, hd, pos):
+    ib, pb, kb, vb = c.upload(inv), c.upload(positions), c.upload(k), c.upload(v)
+    qb, kcb, vcb, ob = c.upload(q), c.upload(kc0), c.upload(vc0), c.zeros(rows * nh * hd * 4)
+    args = (qb, kb, vb, kcb, vcb, bchip.F16, ib, pb, rows, nh, nkv, hd, hd, False, pos)
+    if fused:
+        c.rope_append_attention_rows(*args, 1 / math.sqrt(hd), ob)
+    else:
+        c.rope_append(*args)
+        c.attention(qb, kcb, vcb, bchip.F16, ob, None, False, rows, nh, nkv, hd, pos, 1 / math.sqrt(hd))
+    got = (c.read(ob, (rows, nh, hd)), c.read(qb, q.shape), c.read(kcb, kc0.shape, np.float16),
+           c.read(vcb, vc0.shape, np.float16))
+    for b in (ib, pb, kb, vb, qb, kcb, vcb, ob):
+        b.free()
+    return got
+
+
+@pytest.mark.parametrize("env", [{"BCHIP_GROUP_FOLD": "spread"}, {"BCHIP_GROUP_FOLD": "0"}])
+def test_rows_step_under_the_fold_switches(ctx, env):
+    """The fused step with the group fold's spread path forced (every state published again
+    write-through, a second count), and with the group fold off (the call then runs as its two
+    calls): the same bits as the two calls on the default context, three calls in a row."""
+    rows, nh, nkv, hd, pos = 8, 64, 8, 128, 4096
+    kvd = nkv * hd
+    q, k, v = rand((rows, nh * hd), 21), rand((rows, kvd), 22), rand((rows, kvd), 23)
+    kc0, vc0 = rand((pos + rows, kvd), 24).astype(np.float16), rand((pos + rows, kvd), 25).astype(np.float16)
+    inv = O.inv_freq(hd, 5e5)
+    positions = (pos + np.arange(rows)).astype(np.uint32)
+    want = _step(ctx, False, q, k, v, kc0, vc0, inv, positions, rows, nh, nkv, hd, pos)
+    other = _ctx_with(env)
+    try:
+        for _ in range(3):
+            got = _step(other, True, q, k, v, kc0, vc0, inv, positions, rows, nh, nkv, hd, pos)
+            for name, a, b in zip(("out", "rotated q", "K cache", "V cache"), got, want):
+                np.testing.assert_array_equal(a, b, err_msg=f"{env}: {name}")
+    finally:
+        other.close()
