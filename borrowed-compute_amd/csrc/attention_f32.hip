@@ -50,6 +50,12 @@ struct F32Params {
     const float* zero;  // ZERO_BYTES of zeros: the loads of rows past a list
 };
 
+// The dot's and P v's loops: two steps a trip at hd <= 64 (their LDS reads then go out
+// together; configs[0]'s step 24.9 -> 22.7 us a layer), one at hd 128 (there the same
+// measured slower, 76 -> 77-80 us: the registers cost more than the overlap gives).
+template <int HD>
+constexpr int F32_LU = HD <= 64 ? 2 : 1;
+
 template <int HD>
 __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     // q and K rows in LDS in lane order: element d = j + 8i at j * NI + i, so that the
@@ -204,23 +210,33 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             // across the wave; P of entry k in lane k; the block sum and P v entry by entry
             // in order, P taken from its lane.
             const uint32_t k = lane & 31u, h = lane >> 5;
+            // Slots s0 .. s0 + NS - 1 of the wave together: each slot's operations as alone,
+            // in the same order; K's and V's LDS reads serve all of them.
+            auto pass = [&](auto S0, auto NSc) {
+                constexpr int s0 = decltype(S0)::value, NS = decltype(NSc)::value;
+                uint32_t nn[NS];
+                float a[NS][4];
 #pragma unroll
-            for (int sw = 0; sw < SPW; sw++) {
-                const uint32_t n = wave + W * sw;
-                if (n >= nused) break;
-                float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int s = 0; s < NS; s++) {
+                    nn[s] = wave + W * (s0 + s);
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) a[s][jj] = 0.0f;
+                }
                 // d = j + 8 (i + t) in order; past hd (a head dim below HD) no term.
                 auto dot_lanes = [&](auto FULL) {
-#pragma unroll 1
+#pragma unroll F32_LU<HD>
                     for (uint32_t i = 0; i < (uint32_t)NI; i += 4) {
 #pragma unroll
                         for (uint32_t jj = 0; jj < 4; jj++) {
                             const uint32_t j = 4 * h + jj;
                             const f32x4 kv = *(const f32x4*)&ks[k][j * NI + i];
-                            const f32x4 qv = *(const f32x4*)&qs[n][j * NI + i];
 #pragma unroll
-                            for (uint32_t t = 0; t < 4; t++)
-                                if (decltype(FULL)::value || 8 * (i + t) < hd) a[jj] += qv[t] * kv[t];
+                            for (int s = 0; s < NS; s++) {
+                                const f32x4 qv = *(const f32x4*)&qs[nn[s]][j * NI + i];
+#pragma unroll
+                                for (uint32_t t = 0; t < 4; t++)
+                                    if (decltype(FULL)::value || 8 * (i + t) < hd) a[s][jj] += qv[t] * kv[t];
+                            }
                         }
                     }
                 };
@@ -228,44 +244,86 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
                     dot_lanes(std::true_type{});
                 else
                     dot_lanes(std::false_type{});
-                float dsum = 0.0f + a[0];
-                dsum += a[1];
-                dsum += a[2];
-                dsum += a[3];
+                float pe[NS], mn[NS], cr[NS];
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++) dsum += up32(a[jj]);
-                const float sc = (lane < 32u && key0 + k < slot_len(n)) ? dsum * p.sc : -INFINITY;
-                const float mx = wave_max(sc);
-                const float mn = fmaxf(m[sw], mx), ms = (mn == -INFINITY) ? 0.0f : mn;
-                const float cr = exp2_hw(m[sw] - ms);
-                const float pe = exp2_hw(sc - ms);
-                float bl = 0.0f, acc[DPL];
+                for (int s = 0; s < NS; s++) {
+                    float dsum = 0.0f + a[s][0];
+                    dsum += a[s][1];
+                    dsum += a[s][2];
+                    dsum += a[s][3];
 #pragma unroll
-                for (int dd = 0; dd < DPL; dd++) acc[dd] = 0.0f;
-#pragma unroll 1
+                    for (int jj = 0; jj < 4; jj++) dsum += up32(a[s][jj]);
+                    const float sc = (lane < 32u && key0 + k < slot_len(nn[s])) ? dsum * p.sc : -INFINITY;
+                    const float mx = wave_max(sc);
+                    mn[s] = fmaxf(m[s0 + s], mx);
+                    const float ms = (mn[s] == -INFINITY) ? 0.0f : mn[s];
+                    cr[s] = exp2_hw(m[s0 + s] - ms);
+                    pe[s] = exp2_hw(sc - ms);
+                }
+                float bl[NS], acc[NS][DPL];
+#pragma unroll
+                for (int s = 0; s < NS; s++) {
+                    bl[s] = 0.0f;
+#pragma unroll
+                    for (int dd = 0; dd < DPL; dd++) acc[s][dd] = 0.0f;
+                }
+#pragma unroll F32_LU<HD>
                 for (int k8 = 0; k8 < F32_BLK; k8 += 8) {
 #pragma unroll
-                for (int kj = 0; kj < 8; kj++) {
-                    const int kk = k8 + kj;
-                    const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), kk));
-                    bl += pk;
-                    if constexpr (DPL == 1) {
-                        acc[0] += pk * vs[kk][dl];
-                    } else if constexpr (DPL == 2) {
-                        const float2 v = *(const float2*)&vs[kk][2 * dl];
-                        acc[0] += pk * v.x;
-                        acc[1] += pk * v.y;
-                    } else {
-                        const f32x4 v = *(const f32x4*)&vs[kk][4 * dl];
+                    for (int kj = 0; kj < 8; kj++) {
+                        const int kk = k8 + kj;
+                        float v[DPL];
+                        if constexpr (DPL == 1) {
+                            v[0] = vs[kk][dl];
+                        } else if constexpr (DPL == 2) {
+                            const float2 v2 = *(const float2*)&vs[kk][2 * dl];
+                            v[0] = v2.x;
+                            v[1] = v2.y;
+                        } else {
+                            const f32x4 v4 = *(const f32x4*)&vs[kk][4 * dl];
 #pragma unroll
-                        for (int dd = 0; dd < 4; dd++) acc[dd] += pk * v[dd];
+                            for (int dd = 0; dd < 4; dd++) v[dd] = v4[dd];
+                        }
+#pragma unroll
+                        for (int s = 0; s < NS; s++) {
+                            const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe[s]), kk));
+                            bl[s] += pk;
+#pragma unroll
+                            for (int dd = 0; dd < DPL; dd++) acc[s][dd] += pk * v[dd];
+                        }
                     }
                 }
-                }
-                l[sw] = l[sw] * cr + bl;
-                m[sw] = mn;
 #pragma unroll
-                for (int dd = 0; dd < DPL; dd++) o[sw][dd] = o[sw][dd] * cr + acc[dd];
+                for (int s = 0; s < NS; s++) {
+                    l[s0 + s] = l[s0 + s] * cr[s] + bl[s];
+                    m[s0 + s] = mn[s];
+#pragma unroll
+                    for (int dd = 0; dd < DPL; dd++) o[s0 + s][dd] = o[s0 + s][dd] * cr[s] + acc[s][dd];
+                }
+            };
+            using i0 = std::integral_constant<int, 0>;
+            using i1 = std::integral_constant<int, 1>;
+            using i2 = std::integral_constant<int, 2>;
+            using i3 = std::integral_constant<int, 3>;
+            static_assert(SPW == 4, "four slots a wave at most");
+            // The wave's slots that may hold a query: wave, wave + W, ... below nused.
+            const uint32_t nact = wave < nused ? min((uint32_t)SPW, (nused - wave + W - 1) / W) : 0u;
+            if constexpr (HD <= 64) {
+                // Two slots a pass: the shared reads and the two slots' chains side by side
+                // (configs[0], seven slots over four waves: 22.7 -> 21.9 us a layer-step).
+                if (nact >= 2)
+                    pass(i0{}, i2{});
+                else if (nact == 1)
+                    pass(i0{}, i1{});
+                if (nact >= 4)
+                    pass(i2{}, i2{});
+                else if (nact == 3)
+                    pass(i2{}, i1{});
+            } else {
+                if (nact >= 1) pass(i0{}, i1{});
+                if (nact >= 2) pass(i1{}, i1{});
+                if (nact >= 3) pass(i2{}, i1{});
+                if (nact >= 4) pass(i3{}, i1{});
             }
         }
         if (p.split) break;
