@@ -98,6 +98,22 @@ def test_rows_step_is_rope_append_then_attention(ctx, rows, nh, nkv, hd, rd, neo
         b.free()
 
 
+def test_rows_step_takes_each_rows_position(ctx):
+    """The rotation angles come from positions[r], which need not be the rows' slots (a
+    pipeline stage or a tree numbers its tokens as it likes): rows with scattered positions,
+    fused (configs[4]'s shape) against the two calls, bit for bit."""
+    rows, nh, nkv, hd, pos = 8, 64, 8, 128, 3000
+    kvd = nkv * hd
+    q, k, v = rand((rows, nh * hd), 31), rand((rows, kvd), 32), rand((rows, kvd), 33)
+    kc0, vc0 = rand((pos + rows, kvd), 34).astype(np.float16), rand((pos + rows, kvd), 35).astype(np.float16)
+    inv = O.inv_freq(hd, 5e5)
+    positions = np.array([7, 100000, 3000, 3001, 12, 65535, 40000, 2999], np.uint32)
+    want = _step(ctx, False, q, k, v, kc0, vc0, inv, positions, rows, nh, nkv, hd, pos)
+    got = _step(ctx, True, q, k, v, kc0, vc0, inv, positions, rows, nh, nkv, hd, pos)
+    for name, a, b in zip(("out", "rotated q", "K cache", "V cache"), got, want):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+
+
 def test_rows_step_repeats_bit_for_bit(ctx):
     """Run-to-run determinism of the fused multi-row step (model.rs:648 asks it of every pass)."""
     rows, nh, nkv, hd, pos = 8, 64, 8, 128, 5000
