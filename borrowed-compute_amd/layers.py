@@ -5,7 +5,9 @@ library's entry points instead of a Cmd list.
 
 Per layer, in the reference's order: RMSNorm, the q/k/v products, their biases, RoPE of q
 and k with the append of k and v at slot `pos` (the four commands at mod.rs:464-475 as one
-bchip_rope_append), attention over the cache, the output product and the residual add,
+bchip_rope_append), attention over the cache (for a line pass, with the append as one
+call: bchip_rope_append_attention or its multi-row form), the output product and the
+residual add,
 RMSNorm, gate and up products, SiLU-mul, the down product and the residual add. Weights
 stay in their ggml blocks (bchip_matmul). The cache is a bchip.KvCache (Gpu::reserve's
 growth, mod.rs:404-423); positions and the tree's visibility masks come from the caller's
@@ -152,6 +154,11 @@ class GpuLayers:
                 # A one-token line step: the five commands as one launch (same bits).
                 ctx.rope_append_attention(s["q"], s["k"], s["v"], kc, vc, self.kv_type, self.freq, s["pos"], nh, nkv,
                                           hd, c.rope_dim, c.rope_neox, pos, scale, s["att"])
+            elif masks is None:
+                # A line pass of several rows: one call (one launch where the library can, else
+                # its two calls; the same bits either way).
+                ctx.rope_append_attention_rows(s["q"], s["k"], s["v"], kc, vc, self.kv_type, self.freq, s["pos"], rows,
+                                               nh, nkv, hd, c.rope_dim, c.rope_neox, pos, scale, s["att"])
             else:
                 ctx.rope_append(s["q"], s["k"], s["v"], kc, vc, self.kv_type, self.freq, s["pos"], rows, nh, nkv, hd,
                                 c.rope_dim, c.rope_neox, pos)

@@ -165,3 +165,29 @@ def test_wide_stage_f16_tree_rows_equal_their_lines_and_keep(ctx, model):
     for c in (kv, fresh):
         c.free()
     part.g.free()
+
+
+def test_wide_stage_f16_verify_rows_after_a_long_prefix(ctx, model):
+    """A verify step's draft rows (llm.rs:655-667) after a prefix longer than one 192-slot
+    chunk, so that each layer's rows run as one call of RoPE, append and split attention in
+    one launch: fed as a line and as a chain tree (each row sees the prefix and the rows
+    before it), the same bits row for row (model.rs:578); the line's last row against the
+    text fed whole within one f16 step of the largest score."""
+    part = Part(ctx, model, 0, 3, True, bchip.F16)
+    prefix = [(i * 53 + 7) % 250 + 3 for i in range(230)]
+    drafts = [40, 41, 42, 43, 44, 45, 46, 47]
+    kv_line, kv_tree = part.g.new_cache(), part.g.new_cache()
+    run([part], [kv_line], prefix, 0)
+    run([part], [kv_tree], prefix, 0)
+    line = run([part], [kv_line], drafts, len(prefix))
+    chain = [O.ROOT] + list(range(len(drafts) - 1))
+    x = part.forward(embed(part.embd, drafts), len(prefix), chain, kv_tree)
+    tree = part.g.logits(x, len(drafts))
+    for row in range(len(drafts)):
+        np.testing.assert_array_equal(line[row], tree[row], err_msg=f"draft row {row}")
+    fresh = part.g.new_cache()
+    whole = run([part], [fresh], prefix + drafts, 0)
+    close(line[-1], whole[-1].astype(np.float64), F16_STEP, "verify rows against the text fed whole")
+    for c in (kv_line, kv_tree, fresh):
+        c.free()
+    part.g.free()
