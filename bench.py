@@ -615,7 +615,7 @@ def main():
             log(json.dumps(extra["verify_loop_70b_256_fused"]))
         if "f32" in want:
             # The drop-in default: an unmodified binding passes the reference's f32 cache
-            # (bchip_rope_append_attention with BCHIP_F32: rope_append, then attn_f32).
+            # (bchip_rope_append_attention with BCHIP_F32: attn_f32 with the rotation and the append).
             log(f"f32-cache decode (the reference's cache type): configs[1] at {args.ctx} slots, configs[0]")
             r = bench_decode(ctx, hip, args.ctx, 10, 2, kv_type=bchip.F32)
             r["note"] = "f32 cache, f32 arithmetic (attn_f32): the path an unmodified binding runs"

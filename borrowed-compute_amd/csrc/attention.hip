@@ -1311,6 +1311,37 @@ __global__ __launch_bounds__(64 * W) void attn_shared(const SharedParams p) {
 // loads of RUN chunk states before the first fold step uses them. RUN is the smallest of
 // 8, 16, 24, 32 that holds a shared call's chunks (fewer loads of clamped duplicates: 0.45
 // us off the 70B verify call at 4096 slots), else 32 (one batch up to 8192 entries).
+// An f32 one-row step fused with RoPE (CombineParams::fuse): the fold, which runs once every
+// chunk's workgroup has read q, leaves pair pp of output head h of row r rotated, as
+// k_rope_append rotates q (the same expressions, so the same bits). The long fold loads the
+// pair's operands when it starts (load) and rotates and stores them once it is done (store),
+// so that their round trip overlaps the fold's.
+struct QPair {
+    float x0, x1, f;
+    uint32_t pos, a, b;
+    bool rot;
+};
+__device__ __forceinline__ QPair combine_q_load(const CombineParams& p, uint32_t r, uint32_t h, uint32_t pp) {
+    QPair q{};
+    q.rot = p.fuse && rope_pair(pp, p.rope_dim, p.neox, q.a, q.b);
+    if (q.rot) {
+        const float* qh = p.qw + ((size_t)r * p.nh + h) * p.hd;
+        q.x0 = qh[q.a];
+        q.x1 = qh[q.b];
+        q.f = p.inv_freq[pp];
+        q.pos = p.positions[r];
+    }
+    return q;
+}
+__device__ __forceinline__ void combine_q_store(const CombineParams& p, uint32_t r, uint32_t h, const QPair& q) {
+    if (!q.rot) return;
+    float* qh = p.qw + ((size_t)r * p.nh + h) * p.hd;
+    float y0, y1;
+    rotate(q.x0, q.x1, (float)q.pos * q.f, y0, y1);
+    qh[q.a] = y0;
+    qh[q.b] = y1;
+}
+
 constexpr int CMB_RUN = 32;
 
 constexpr int CMB_THREADS = 64;
@@ -1373,6 +1404,9 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine(const CombineParams 
         }
     }
     *(float4*)(p.out + ((size_t)r * p.nh + h) * p.hd + 4 * d4) = float4{O.x / L, O.y / L, O.z / L, O.w / L};
+    // (Here the pairs' loads measured no slower than at the start: a short fold.)
+    combine_q_store(p, r, h, combine_q_load(p, r, h, 2 * d4));
+    combine_q_store(p, r, h, combine_q_load(p, r, h, 2 * d4 + 1));
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1448,6 +1482,7 @@ __global__ __launch_bounds__(CMBL_THREADS) void attn_combine_long(const CombineP
     const uint32_t stride = p.slots;  // partial slots per unit
     auto state = [&](uint32_t c) { return (unit0 + c * step) * stride + slot; };
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const QPair qp = combine_q_load(p, r, h, tid < hd / 2 ? tid : 0u);
     typedef __attribute__((address_space(3))) void lds_t;
     // Barriers without a fence: the waits before them are explicit (a fence would wait for
     // every direct-to-LDS load in flight, the states' included).
@@ -1548,6 +1583,7 @@ __global__ __launch_bounds__(CMBL_THREADS) void attn_combine_long(const CombineP
         L = lfin;
     }
     if (tid < hd) p.out[((size_t)r * p.nh + h) * hd + tid] = O / L;
+    if (tid < hd / 2) combine_q_store(p, r, h, qp);
 }
 
 // V^T tiles of a prefill call (written by vt_pack): per KV head, hd rows of npad keys, each

@@ -48,6 +48,16 @@ struct F32Params {
     uint32_t nchunk;  // chunks of the farthest list
     uint32_t split;   // a workgroup per chunk
     const float* zero;  // ZERO_BYTES of zeros: the loads of rows past a list
+    // A one-row step fused with RoPE and the K/V append of its row at slot pos (attn_f32<HD,
+    // true>): q is unrotated on entry and rotated as it is staged; the new K row (knew,
+    // rotated here) and V row (vnew) go to the caches at slot pos and stand in for that slot's
+    // cache entry. q is left rotated: by the workgroup itself when unsplit, else by the fold.
+    const float* knew;
+    const float* vnew;
+    const float* inv_freq;
+    const uint32_t* positions;  // positions[0]: the row's rotation position
+    uint32_t rope_dim, neox;
+    float* qw;
 };
 
 // The dot's and P v's loops: two steps a trip at hd <= 64 (their LDS reads then go out
@@ -56,7 +66,7 @@ struct F32Params {
 template <int HD>
 constexpr int F32_LU = HD <= 64 ? 2 : 1;
 
-template <int HD>
+template <int HD, bool FUSE>
 __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     // q and K rows in LDS in lane order: element d = j + 8i at j * NI + i, so that the
     // elements of quant::dot's lane j (d = j, j + 8, ...) are contiguous and read 16 bytes at a
@@ -77,6 +87,8 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     __shared__ __attribute__((aligned(16))) float ks[F32_BLK][KS];
     __shared__ __attribute__((aligned(16))) float vs[F32_BLK][HD];
     __shared__ uint32_t tail[MAX_ITEMS];
+    // FUSE: the new K row (rotated) and V row as the caches hold them.
+    __shared__ __attribute__((aligned(16))) float nrow[FUSE ? 2 : 1][FUSE ? HD : 4];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t gi = p.split ? blockIdx.x / p.nchunk : blockIdx.x;
@@ -143,16 +155,24 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             vr[i] = *(gf4*)va;
         }
     };
-    auto stash = [&]() {
+    auto stash = [&](uint32_t key0) {
 #pragma unroll
         for (int i = 0; i < NL; i++) {
             const uint32_t e = tid + F32_THREADS * i, k = e / (HD / 4), d = 4 * (e % (HD / 4));
+            f32x4 kx = kr[i], vx = vr[i];
+            if constexpr (FUSE) {
+                // The new row's slot: its K and V as this kernel wrote them to the caches.
+                if (key0 + k == p.pos) {
+                    kx = *(const f32x4*)&nrow[0][d];
+                    vx = *(const f32x4*)&nrow[1][d];
+                }
+            }
             float* kd = &ks[k][(d % 8) * NI + d / 8];  // d % 8 is 0 or 4: elements d .. d + 3 are lanes' runs apart
-            kd[0] = kr[i][0];
-            kd[NI] = kr[i][1];
-            kd[2 * NI] = kr[i][2];
-            kd[3 * NI] = kr[i][3];
-            *(f32x4*)&vs[k][d] = vr[i];
+            kd[0] = kx[0];
+            kd[NI] = kx[1];
+            kd[2 * NI] = kx[2];
+            kd[3 * NI] = kx[3];
+            *(f32x4*)&vs[k][d] = vx;
         }
     };
     const uint32_t nused = used_e / HD;  // slots that may hold a query
@@ -178,20 +198,82 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     if (p.tree) __syncthreads();
     const uint32_t cend = p.split ? c_one + 1u : max(1u, (maxlen + CHUNK_MULTI - 1u) / CHUNK_MULTI);
     if (c_one * CHUNK_MULTI < maxlen) fetch(c_one * CHUNK_MULTI, min(c_one * CHUNK_MULTI + CHUNK_MULTI, maxlen));
-    for (uint32_t e = tid; e < F32_SLOTS * HD; e += F32_THREADS) {
-        const uint32_t n = e / HD, d = e % HD;
-        float v = 0.0f;
-        if (d < hd && slot_valid(n)) {
-            const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
-            v = p.q[((size_t)r * p.nh + h) * hd + d];
+    if constexpr (FUSE) {
+        // One row at slot pos: its position's angles; pair pp of a head is (a, b) by rope_pair,
+        // rotated when pp < rope_dim / 2 by k_rope_append's expressions (the same bits).
+        const float posf = (float)p.positions[0];
+        const size_t kvd_s = kvd;
+        if (c_one * CHUNK_MULTI <= p.pos && p.pos < cend * CHUNK_MULTI && tid < (uint32_t)HD / 2) {
+            // This workgroup streams the new slot: K rotated and V, into the caches and nrow.
+            const uint32_t pp = tid;
+            uint32_t a, b;
+            const bool rot = rope_pair(pp, p.rope_dim, p.neox, a, b);
+            float k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
+            if (pp < hd / 2) {
+                const float* kx = p.knew + (size_t)kvh * hd;
+                const float* vx = p.vnew + (size_t)kvh * hd;
+                k0 = kx[a];
+                k1 = kx[b];
+                if (rot) rotate(kx[a], kx[b], posf * p.inv_freq[pp], k0, k1);
+                v0 = vx[2 * pp];
+                v1 = vx[2 * pp + 1];
+                float* kdst = (float*)p.kc + (size_t)p.pos * kvd_s + (size_t)kvh * hd;
+                float* vdst = (float*)p.vc + (size_t)p.pos * kvd_s + (size_t)kvh * hd;
+                kdst[a] = k0;
+                kdst[b] = k1;
+                vdst[2 * pp] = v0;
+                vdst[2 * pp + 1] = v1;
+            }
+            nrow[0][a] = k0;
+            nrow[0][b] = k1;
+            nrow[1][2 * pp] = v0;
+            nrow[1][2 * pp + 1] = v1;
         }
-        qs[n][(d % 8) * NI + d / 8] = v;
+        // q rotated as it is staged, a pair a thread (dims past hd and empty slots: zeros).
+        for (uint32_t e = tid; e < F32_SLOTS * (HD / 2); e += F32_THREADS) {
+            const uint32_t n = e / (HD / 2), pp = e % (HD / 2);
+            uint32_t a, b;
+            const bool rot = rope_pair(pp, p.rope_dim, p.neox, a, b);
+            float y0 = 0.0f, y1 = 0.0f;
+            if (pp < hd / 2 && slot_valid(n)) {
+                const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
+                const float* qh = p.q + ((size_t)r * p.nh + h) * hd;
+                y0 = qh[a];
+                y1 = qh[b];
+                if (rot) rotate(qh[a], qh[b], posf * p.inv_freq[pp], y0, y1);
+            }
+            qs[n][(a % 8) * NI + a / 8] = y0;
+            qs[n][(b % 8) * NI + b / 8] = y1;
+        }
+        if (!p.split) {
+            // q stays rotated, as k_rope_append leaves it: this workgroup is the only reader of
+            // its heads, and every read of them is done at the barrier. (A split launch's fold
+            // writes them once every chunk's workgroup has read them.)
+            __syncthreads();
+            for (uint32_t e = tid; e < F32_SLOTS * HD; e += F32_THREADS) {
+                const uint32_t n = e / HD, d = e % HD;
+                if (d < hd && slot_valid(n)) {
+                    const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
+                    p.qw[((size_t)r * p.nh + h) * hd + d] = qs[n][(d % 8) * NI + d / 8];
+                }
+            }
+        }
+    } else {
+        for (uint32_t e = tid; e < F32_SLOTS * HD; e += F32_THREADS) {
+            const uint32_t n = e / HD, d = e % HD;
+            float v = 0.0f;
+            if (d < hd && slot_valid(n)) {
+                const uint32_t r = r0 + n % p.rb, h = kvh * p.G + n / p.rb;
+                v = p.q[((size_t)r * p.nh + h) * hd + d];
+            }
+            qs[n][(d % 8) * NI + d / 8] = v;
+        }
     }
     for (uint32_t c = c_one; c < cend; c++) {
         const uint32_t kb0 = c * CHUNK_MULTI, kb1 = min(kb0 + CHUNK_MULTI, maxlen);
         for (uint32_t key0 = kb0; key0 < kb1; key0 += F32_BLK) {
             __syncthreads();  // the previous block's K, V and P are consumed (and q is in)
-            stash();
+            stash(key0);
             if (key0 + F32_BLK < kb1) {
                 fetch(key0 + F32_BLK, kb1);
             } else if (c + 1 < cend && kb1 < maxlen) {
@@ -374,16 +456,32 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
 static uint32_t ceil_div32(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
 template <int HD>
-static hipError_t launch_f32_t(const F32Params& fp, uint32_t blocks, const AttnCall& a, hipStream_t s) {
-    hipExtLaunchKernelGGL((attn_f32<HD>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0, fp);
+static hipError_t launch_f32_t(const F32Params& fp, uint32_t blocks, const AttnCall& a, hipStream_t s, bool fuse) {
+    if (fuse)
+        hipExtLaunchKernelGGL((attn_f32<HD, true>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0,
+                              fp);
+    else
+        hipExtLaunchKernelGGL((attn_f32<HD, false>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0,
+                              fp);
     return hipGetLastError();
 }
 
-hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipStream_t s) {
+hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipStream_t s, const RopeArgs* rope) {
     if (a.rows == 0 || a.nkv == 0 || a.nh % a.nkv != 0 || a.hd == 0 || a.hd % 8 != 0 || a.hd > MAX_HD)
         return hipErrorInvalidValue;
     if (a.tree && a.rows > MAX_ITEMS) return hipErrorInvalidValue;
+    if (rope && (a.tree || a.rows != 1 || kvoff != 0 || rope->rope_dim % 2 || rope->rope_dim > a.hd))
+        return hipErrorInvalidValue;
     F32Params fp{};
+    if (rope) {
+        fp.knew = rope->k;
+        fp.vnew = rope->v;
+        fp.inv_freq = rope->inv_freq;
+        fp.positions = rope->positions;
+        fp.rope_dim = rope->rope_dim;
+        fp.neox = rope->neox;
+        fp.qw = rope->q;
+    }
     const uint64_t kvd = (uint64_t)a.nkv * a.hd;
     fp.q = a.q;
     fp.kc = (const float*)a.kc + kvoff * kvd;
@@ -426,10 +524,10 @@ hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipSt
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
     hipError_t e;
     switch (hdp) {
-        case 32: e = launch_f32_t<32>(fp, (uint32_t)blocks, a, s); break;
-        case 64: e = launch_f32_t<64>(fp, (uint32_t)blocks, a, s); break;
-        case 128: e = launch_f32_t<128>(fp, (uint32_t)blocks, a, s); break;
-        default: e = launch_f32_t<256>(fp, (uint32_t)blocks, a, s); break;
+        case 32: e = launch_f32_t<32>(fp, (uint32_t)blocks, a, s, rope != nullptr); break;
+        case 64: e = launch_f32_t<64>(fp, (uint32_t)blocks, a, s, rope != nullptr); break;
+        case 128: e = launch_f32_t<128>(fp, (uint32_t)blocks, a, s, rope != nullptr); break;
+        default: e = launch_f32_t<256>(fp, (uint32_t)blocks, a, s, rope != nullptr); break;
     }
     if (e != hipSuccess || !fp.split) return e;
     CombineParams cp{};
@@ -449,6 +547,14 @@ hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipSt
     cp.rb = fp.rb;
     cp.nrb = fp.nrb;
     cp.nchunk = fp.nchunk;
+    if (rope) {
+        cp.fuse = 1;
+        cp.qw = rope->q;
+        cp.inv_freq = rope->inv_freq;
+        cp.positions = rope->positions;
+        cp.rope_dim = rope->rope_dim;
+        cp.neox = rope->neox;
+    }
     return combine_launch(cp, (uint32_t)groups, a.hd, s);
 }
 

@@ -748,20 +748,22 @@ static int fused_step(bchip_ctx* c, Workspace& ws, float* q, const float* k, con
     const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
     AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, 1u, nh, nkv, hd, pos, scale, limit};
     c->take_marks(a);
+    if (kv_type == BCHIP_F32) {
+        // f32 caches: attn_f32 rotates q and appends the new row itself (the two calls' bits).
+        const RopeArgs r{q, k, v, inv_freq, positions, rope_dim, neox};
+        HIP_TRY(f32_attention(a, 0, ws, c->stream, &r), "rope_append_attention");
+        return BCHIP_OK;
+    }
     if (!fuse) {
-        // f32 caches, and shapes the fused kernel does not take: the two calls.
+        // Shapes the fused kernel does not take: the two calls.
         HIP_TRY(rope_append_launch(q, k, v, kc, vc, kv_type, inv_freq, positions, 1, nh, nkv, hd, rope_dim, neox,
                                    pos, c->stream),
                 "rope_append");
-        if (kv_type == BCHIP_F32) {
-            HIP_TRY(f32_attention(a, 0, ws, c->stream), "attention");
-        } else {
-            Item item{};
-            item.row = 0;
-            item.nrows = 1;
-            item.len = (uint32_t)slots;
-            HIP_TRY(row_attention(a, &item, 1, ws, c->stream), "attention");
-        }
+        Item item{};
+        item.row = 0;
+        item.nrows = 1;
+        item.len = (uint32_t)slots;
+        HIP_TRY(row_attention(a, &item, 1, ws, c->stream), "attention");
         return BCHIP_OK;
     }
     RopeArgs r{q, k, v, inv_freq, positions, rope_dim, neox};

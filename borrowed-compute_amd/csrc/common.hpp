@@ -194,6 +194,12 @@ struct CombineParams {
     uint32_t ngroups;  // groups in the launch
     uint32_t nitems;
     uint32_t long_fold;  // host: lists of more than CMB_RUN chunks may take attn_combine_long
+    // An f32 one-row step fused with RoPE (fuse != 0): the fold leaves each output slot's q
+    // head rotated (k_rope_append's expressions), every chunk's workgroup having read it.
+    uint32_t fuse, rope_dim, neox;
+    float* qw;
+    const float* inv_freq;
+    const uint32_t* positions;
     Item items[MAX_ITEMS];
 };
 

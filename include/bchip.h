@@ -152,9 +152,10 @@ int bchip_attention(bchip_ctx* ctx, const float* q, const void* kc, const void* 
  * bit for bit (out; q left rotated; the new row in kc and vc). It is the peephole over the
  * five commands k_rope(q), k_rope(k), k_copy(k), k_copy(v), k_attention that
  * Layers::forward queues per layer for a one-token pass (gpu/mod.rs:464-482): the rotation
- * and the append run inside the attention kernel, which takes the new row from registers.
- * f32 caches, and shapes the fused kernel does not take (hd % 32 != 0, neox pairs with
- * rope_dim/2 not a multiple of 32, or more than 8 query heads per KV head), run as the two
+ * and the append run inside the attention kernel, which takes the new row from registers
+ * (f16 caches) or LDS (f32 caches: attn_f32 rotates q as it stages it and the fold leaves q
+ * rotated). f16 shapes the fused kernel does not take (hd % 32 != 0, neox pairs with
+ * rope_dim/2 not a multiple of 32, or more than 8 query heads per KV head) run as the two
  * calls. positions: device u32 [1]. */
 int bchip_rope_append_attention(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
                                 uint32_t kv_type, const float* inv_freq, const uint32_t* positions, uint32_t nh,

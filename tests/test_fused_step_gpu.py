@@ -39,7 +39,15 @@ CASES = [
     (64, 8, 128, 128, False, 5e5, bchip.F16, 6136),    # configs[4] heads
     (8, 8, 256, 256, False, 1e4, bchip.F16, 700),      # head_dim 256
     (32, 8, 128, 96, True, 5e5, bchip.F16, 100),       # neox pairs 48 apart: the two-call path
-    (4, 2, 16, 16, False, 1e4, bchip.F32, 6),          # tiny_model shape (hd 16): the two-call path
+    (4, 2, 16, 16, False, 1e4, bchip.F32, 6),          # tiny_model shape (hd 16), f32 cache
+    (32, 8, 128, 128, False, 5e5, bchip.F32, 0),       # f32 cache: the first token (unsplit, q by the kernel)
+    (32, 8, 128, 128, False, 5e5, bchip.F32, 192),     # f32: the new row alone in the last chunk
+    (32, 8, 128, 128, False, 5e5, bchip.F32, 4000),    # f32: split, q rotated by attn_combine
+    (32, 8, 128, 128, False, 5e5, bchip.F32, 32767),   # configs[1] over an f32 cache (attn_combine_long)
+    (28, 4, 128, 96, True, 1e6, bchip.F32, 3000),      # f32: neox pairs 48 apart, partial rotary
+    (8, 8, 256, 128, False, 1e4, bchip.F32, 700),      # f32: head_dim 256, partial rotary
+    (14, 2, 64, 32, True, 1e6, bchip.F32, 300),        # f32: hd 64, neox over half the dims
+    (16, 1, 64, 64, False, 1e4, bchip.F32, 100),       # f32: 16 query heads per KV head
     (16, 1, 128, 128, False, 5e5, bchip.F16, 200),     # 16 query heads per KV head: the two-call path
     (16, 2, 128, 128, False, 5e5, bchip.F16, 256),     # 8 per KV head, the last chunk holds the new row alone
 ]

@@ -45,8 +45,9 @@ def step(ctx, noalloc, nh, nkv, hd, rd, neox, theta, kv_type, pos, seed):
 PAIRS = [
     ((32, 8, 128, 128, False, 5e5, bchip.F16, 32767), (32, 8, 128, 128, False, 5e5, bchip.F16, 1000)),
     ((8, 8, 256, 256, False, 1e4, bchip.F16, 20000), (28, 4, 128, 128, True, 1e6, bchip.F16, 3000)),
-    # f32 caches: the two-call path; 60001 slots take more chunk states than the scratch holds
-    # (then unsplit: the same bits as the split pass of the allocating entry point).
+    # f32 caches (attn_f32 rotating q and appending the row itself); 60001 slots take more
+    # chunk states than the scratch holds (then unsplit, q written back by the kernel: the
+    # same bits as the split pass of the allocating entry point, q rotated by its fold).
     ((32, 8, 128, 128, False, 5e5, bchip.F32, 60000), (14, 2, 64, 64, True, 1e6, bchip.F32, 511)),
     # Shapes the fused kernel does not take: rope_append, then the one-row kernel.
     ((16, 1, 128, 128, False, 5e5, bchip.F16, 9000), (32, 8, 128, 96, True, 5e5, bchip.F16, 100)),
