@@ -170,8 +170,8 @@ int bchip_rope_append_attention(bchip_ctx* ctx, float* q, const float* k, const 
  * queues per layer for a pass of several rows (gpu/mod.rs:464-482). One launch does the
  * rotations, the appends and the attention (its workgroups take the new rows from LDS) for
  * f16 caches at head_dim 128, at most 16 rows with rows x (nh / nkv) <= 64, a line longer
- * than one 192-slot chunk whose split launch fits the device's CUs at once, and neox pairs
- * only at rope_dim 64 or 128; other shapes run as the two calls.
+ * than one 192-slot chunk whose split launch fits the device's CUs at once, neox pairs
+ * only at rope_dim 64 or 128, and k and v 16-byte aligned; other calls run as the two calls.
  * positions: device u32 [rows]. */
 int bchip_rope_append_attention_rows(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
                                      uint32_t kv_type, const float* inv_freq, const uint32_t* positions,

@@ -114,6 +114,36 @@ def test_rows_step_takes_each_rows_position(ctx):
         np.testing.assert_array_equal(a, b, err_msg=name)
 
 
+def test_rows_step_with_unaligned_new_rows(ctx):
+    """k and v 4 bytes past a 16-byte boundary: the one-launch form loads them 16 bytes a lane,
+    so the call runs as its two calls; the same bits as those."""
+    rows, nh, nkv, hd, pos = 8, 64, 8, 128, 4096
+    kvd = nkv * hd
+    q, k, v = rand((rows, nh * hd), 41), rand((rows, kvd), 42), rand((rows, kvd), 43)
+    kc0, vc0 = rand((pos + rows, kvd), 44).astype(np.float16), rand((pos + rows, kvd), 45).astype(np.float16)
+    ib = ctx.upload(O.inv_freq(hd, 5e5))
+    pb = ctx.upload((pos + np.arange(rows)).astype(np.uint32))
+    kb, vb = ctx.zeros(k.nbytes + 16), ctx.zeros(v.nbytes + 16)
+    ctx.upload(k, kb, 4)
+    ctx.upload(v, vb, 4)
+    outs = []
+    for fused in (False, True):
+        qb, kcb, vcb, ob = ctx.upload(q), ctx.upload(kc0), ctx.upload(vc0), ctx.zeros(rows * nh * hd * 4)
+        args = (qb, kb.ptr + 4, vb.ptr + 4, kcb, vcb, bchip.F16, ib, pb, rows, nh, nkv, hd, hd, False, pos)
+        if fused:
+            ctx.rope_append_attention_rows(*args, 1 / math.sqrt(hd), ob)
+        else:
+            ctx.rope_append(*args)
+            ctx.attention(qb, kcb, vcb, bchip.F16, ob, None, False, rows, nh, nkv, hd, pos, 1 / math.sqrt(hd))
+        outs.append((ctx.read(ob, (rows, nh, hd)), ctx.read(qb, q.shape), ctx.read(kcb, kc0.shape, np.float16)))
+        for b in (qb, kcb, vcb, ob):
+            b.free()
+    for name, a, b in zip(("out", "rotated q", "K cache"), outs[1], outs[0]):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+    for b in (ib, pb, kb, vb):
+        b.free()
+
+
 def test_rows_step_repeats_bit_for_bit(ctx):
     """Run-to-run determinism of the fused multi-row step (model.rs:648 asks it of every pass)."""
     rows, nh, nkv, hd, pos = 8, 64, 8, 128, 5000
