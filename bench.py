@@ -238,21 +238,24 @@ def bench_multirow(ctx, hip, rows, pos, nh, nkv, hd, reps, n_layer=1, verify=Fal
     return res
 
 
-def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=128, rows=8, fused=False):
+def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=128, rows=8, fused=False,
+                      kv_type=bchip.F16):
     """configs[4]'s speculative decode as configured: 256 steps, each a pass of 8 draft rows
     through the stage's 20 layers, every layer the reference's attention sub-sequence
     (gpu/mod.rs:464-482) for 8 rows: bchip_rope_append (RoPE of q and k, the K/V append at the
     rows' slots) then bchip_attention over the line, or (fused) the one call that stands for
     both, bchip_rope_append_attention_rows (the same bits); all drafts accepted, so the context
     grows 4096 -> 6136 by 8 a step. Timed as one region: the stream time of all 256 x 20
-    layer-steps."""
+    layer-steps. kv_type: the cache's element type (f16 as configured; f32 is the reference's
+    own cache, what an unmodified binding passes)."""
     kvd = nkv * hd
     cap = ctx0 + steps * rows
+    es = 2 if kv_type == bchip.F16 else 4
     kcs, vcs = [], []
     for layer in range(n_layer):
-        k, v = ctx.zeros(cap * kvd * 2), ctx.zeros(cap * kvd * 2)
-        ctx.fill_normal(k, bchip.F16, ctx0 * kvd, 700 + 2 * layer)
-        ctx.fill_normal(v, bchip.F16, ctx0 * kvd, 701 + 2 * layer)
+        k, v = ctx.zeros(cap * kvd * es), ctx.zeros(cap * kvd * es)
+        ctx.fill_normal(k, kv_type, ctx0 * kvd, 700 + 2 * layer)
+        ctx.fill_normal(v, kv_type, ctx0 * kvd, 701 + 2 * layer)
         kcs.append(k)
         vcs.append(v)
     per = rows * (nh + 2 * nkv) * hd  # a layer's q [rows][nh*hd], then k and v [rows][kvd]
@@ -270,12 +273,12 @@ def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=12
             k = q + rows * nh * hd * 4
             v = k + rows * kvd * 4
             if fused:
-                ctx.rope_append_attention_rows(q, k, v, kcs[layer], vcs[layer], bchip.F16, inv, pos.ptr + 4 * s * rows,
+                ctx.rope_append_attention_rows(q, k, v, kcs[layer], vcs[layer], kv_type, inv, pos.ptr + 4 * s * rows,
                                                rows, nh, nkv, hd, hd, False, base, scale, out)
                 continue
-            ctx.rope_append(q, k, v, kcs[layer], vcs[layer], bchip.F16, inv, pos.ptr + 4 * s * rows, rows, nh, nkv,
+            ctx.rope_append(q, k, v, kcs[layer], vcs[layer], kv_type, inv, pos.ptr + 4 * s * rows, rows, nh, nkv,
                             hd, hd, False, base)
-            ctx.attention(q, kcs[layer], vcs[layer], bchip.F16, out, None, False, rows, nh, nkv, hd, base, scale)
+            ctx.attention(q, kcs[layer], vcs[layer], kv_type, out, None, False, rows, nh, nkv, hd, base, scale)
 
     step(0)  # warm (the step's appends are rewritten by the timed step 0)
     ctx.sync()
@@ -285,9 +288,10 @@ def bench_verify_loop(ctx, steps=256, ctx0=4096, n_layer=20, nh=64, nkv=8, hd=12
     total_ms = ctx.timer_stop()
     for b in kcs + vcs + [qkv, pos, inv, out]:
         b.free()
-    kv_bytes = sum(2.0 * (ctx0 + (s + 1) * rows) * kvd * 2 for s in range(steps)) * n_layer
+    kv_bytes = sum(2.0 * (ctx0 + (s + 1) * rows) * kvd * es for s in range(steps)) * n_layer
     layer_steps = steps * n_layer
     return {"steps": steps, "rows": rows, "ctx": [ctx0, ctx0 + steps * rows], "layers": n_layer,
+            "cache": "f16" if kv_type == bchip.F16 else "f32",
             "calls_per_layer_step": "bchip_rope_append_attention_rows" if fused else "bchip_rope_append + bchip_attention",
             "total_ms": total_ms,
             "us_per_layer_step": total_ms * 1e3 / layer_steps,
@@ -625,6 +629,10 @@ def main():
                              neox=True, kv_type=bchip.F32)
             r["note"] = "configs[0]: Qwen2.5-0.5B-shaped, f32 cache at 512 slots, 24 layers; cache-resident"
             extra["decode_qwen05b_512_f32"] = r
+            log(json.dumps(r))
+            log("configs[4]'s verify loop over f32 caches (one call a layer-step)")
+            r = bench_verify_loop(ctx, fused=True, kv_type=bchip.F32)
+            extra["verify_loop_70b_256_f32"] = r
             log(json.dumps(r))
         if "calib" in want:
             extra["copy_calibration"] = bench_copy_calibration(ctx, hip)
