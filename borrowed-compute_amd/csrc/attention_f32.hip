@@ -48,14 +48,15 @@ struct F32Params {
     uint32_t nchunk;  // chunks of the farthest list
     uint32_t split;   // a workgroup per chunk
     const float* zero;  // ZERO_BYTES of zeros: the loads of rows past a list
-    // A one-row step fused with RoPE and the K/V append of its row at slot pos (attn_f32<HD,
-    // true>): q is unrotated on entry and rotated as it is staged; the new K row (knew,
-    // rotated here) and V row (vnew) go to the caches at slot pos and stand in for that slot's
-    // cache entry. q is left rotated: by the workgroup itself when unsplit, else by the fold.
+    // A line call fused with RoPE and the K/V append of its rows at slots pos .. pos + rows - 1
+    // (attn_f32<HD, NR>, NR > 0: at most NR rows): q is unrotated on entry and rotated as it
+    // is staged; the new K rows (knew, rotated here) and V rows (vnew) go to the caches and
+    // stand in for those slots' cache entries. q is left rotated: by the workgroup itself when
+    // unsplit, else by the fold.
     const float* knew;
     const float* vnew;
     const float* inv_freq;
-    const uint32_t* positions;  // positions[0]: the row's rotation position
+    const uint32_t* positions;  // positions[r]: row r's rotation position
     uint32_t rope_dim, neox;
     float* qw;
 };
@@ -66,8 +67,14 @@ struct F32Params {
 template <int HD>
 constexpr int F32_LU = HD <= 64 ? 2 : 1;
 
-template <int HD, bool FUSE>
+// Rows a fused line call of several rows takes (their K and V rows sit in LDS: at 8 rows and
+// hd 128 three workgroups still fit a CU; 16 rows left two, and a verify pass's 704
+// workgroups then took two turns of the GPU, 73 -> 96 us a layer-step).
+constexpr uint32_t F32_FUSE_ROWS = 8;
+
+template <int HD, int NR>
 __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
+    constexpr bool FUSE = NR > 0;
     // q and K rows in LDS in lane order: element d = j + 8i at j * NI + i, so that the
     // elements of quant::dot's lane j (d = j, j + 8, ...) are contiguous and read 16 bytes at a
     // time. Rows are KS floats apart, 4 more than a multiple of 32 banks, so that the eight
@@ -87,8 +94,8 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     __shared__ __attribute__((aligned(16))) float ks[F32_BLK][KS];
     __shared__ __attribute__((aligned(16))) float vs[F32_BLK][HD];
     __shared__ uint32_t tail[MAX_ITEMS];
-    // FUSE: the new K row (rotated) and V row as the caches hold them.
-    __shared__ __attribute__((aligned(16))) float nrow[FUSE ? 2 : 1][FUSE ? HD : 4];
+    // FUSE: the new K rows (rotated) and V rows as the caches hold them.
+    __shared__ __attribute__((aligned(16))) float nrow[FUSE ? 2 : 1][FUSE ? NR : 1][FUSE ? HD : 4];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t gi = p.split ? blockIdx.x / p.nchunk : blockIdx.x;
@@ -161,10 +168,11 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             const uint32_t e = tid + F32_THREADS * i, k = e / (HD / 4), d = 4 * (e % (HD / 4));
             f32x4 kx = kr[i], vx = vr[i];
             if constexpr (FUSE) {
-                // The new row's slot: its K and V as this kernel wrote them to the caches.
-                if (key0 + k == p.pos) {
-                    kx = *(const f32x4*)&nrow[0][d];
-                    vx = *(const f32x4*)&nrow[1][d];
+                // A new row's slot: its K and V as this kernel wrote them to the caches.
+                const uint32_t j = key0 + k - p.pos;
+                if (key0 + k >= p.pos && j < p.rows) {
+                    kx = *(const f32x4*)&nrow[0][j][d];
+                    vx = *(const f32x4*)&nrow[1][j][d];
                 }
             }
             float* kd = &ks[k][(d % 8) * NI + d / 8];  // d % 8 is 0 or 4: elements d .. d + 3 are lanes' runs apart
@@ -199,35 +207,39 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     const uint32_t cend = p.split ? c_one + 1u : max(1u, (maxlen + CHUNK_MULTI - 1u) / CHUNK_MULTI);
     if (c_one * CHUNK_MULTI < maxlen) fetch(c_one * CHUNK_MULTI, min(c_one * CHUNK_MULTI + CHUNK_MULTI, maxlen));
     if constexpr (FUSE) {
-        // One row at slot pos: its position's angles; pair pp of a head is (a, b) by rope_pair,
-        // rotated when pp < rope_dim / 2 by k_rope_append's expressions (the same bits).
-        const float posf = (float)p.positions[0];
+        // Row j's new slot is pos + j, its angles from positions[j]; pair pp of a head is (a, b)
+        // by rope_pair, rotated when pp < rope_dim / 2 by k_rope_append's expressions (the
+        // same bits).
         const size_t kvd_s = kvd;
-        if (c_one * CHUNK_MULTI <= p.pos && p.pos < cend * CHUNK_MULTI && tid < (uint32_t)HD / 2) {
-            // This workgroup streams the new slot: K rotated and V, into the caches and nrow.
-            const uint32_t pp = tid;
-            uint32_t a, b;
-            const bool rot = rope_pair(pp, p.rope_dim, p.neox, a, b);
-            float k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
-            if (pp < hd / 2) {
-                const float* kx = p.knew + (size_t)kvh * hd;
-                const float* vx = p.vnew + (size_t)kvh * hd;
-                k0 = kx[a];
-                k1 = kx[b];
-                if (rot) rotate(kx[a], kx[b], posf * p.inv_freq[pp], k0, k1);
-                v0 = vx[2 * pp];
-                v1 = vx[2 * pp + 1];
-                float* kdst = (float*)p.kc + (size_t)p.pos * kvd_s + (size_t)kvh * hd;
-                float* vdst = (float*)p.vc + (size_t)p.pos * kvd_s + (size_t)kvh * hd;
-                kdst[a] = k0;
-                kdst[b] = k1;
-                vdst[2 * pp] = v0;
-                vdst[2 * pp + 1] = v1;
+        const uint32_t lo = max(c_one * CHUNK_MULTI, p.pos), hi = min(cend * CHUNK_MULTI, p.pos + p.rows);
+        if (lo < hi) {
+            // This workgroup streams new slots lo .. hi - 1: their K rows rotated and V rows,
+            // into the caches and nrow (row blocks of the same chunk write the same values).
+            for (uint32_t e = tid; e < (hi - lo) * (HD / 2); e += F32_THREADS) {
+                const uint32_t j = lo - p.pos + e / (HD / 2), pp = e % (HD / 2);
+                uint32_t a, b;
+                const bool rot = rope_pair(pp, p.rope_dim, p.neox, a, b);
+                float k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
+                if (pp < hd / 2) {
+                    const float* kx = p.knew + ((size_t)j * p.nkv + kvh) * hd;
+                    const float* vx = p.vnew + ((size_t)j * p.nkv + kvh) * hd;
+                    k0 = kx[a];
+                    k1 = kx[b];
+                    if (rot) rotate(kx[a], kx[b], (float)p.positions[j] * p.inv_freq[pp], k0, k1);
+                    v0 = vx[2 * pp];
+                    v1 = vx[2 * pp + 1];
+                    float* kdst = (float*)p.kc + (size_t)(p.pos + j) * kvd_s + (size_t)kvh * hd;
+                    float* vdst = (float*)p.vc + (size_t)(p.pos + j) * kvd_s + (size_t)kvh * hd;
+                    kdst[a] = k0;
+                    kdst[b] = k1;
+                    vdst[2 * pp] = v0;
+                    vdst[2 * pp + 1] = v1;
+                }
+                nrow[0][j][a] = k0;
+                nrow[0][j][b] = k1;
+                nrow[1][j][2 * pp] = v0;
+                nrow[1][j][2 * pp + 1] = v1;
             }
-            nrow[0][a] = k0;
-            nrow[0][b] = k1;
-            nrow[1][2 * pp] = v0;
-            nrow[1][2 * pp + 1] = v1;
         }
         // q rotated as it is staged, a pair a thread (dims past hd and empty slots: zeros).
         for (uint32_t e = tid; e < F32_SLOTS * (HD / 2); e += F32_THREADS) {
@@ -240,7 +252,7 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
                 const float* qh = p.q + ((size_t)r * p.nh + h) * hd;
                 y0 = qh[a];
                 y1 = qh[b];
-                if (rot) rotate(qh[a], qh[b], posf * p.inv_freq[pp], y0, y1);
+                if (rot) rotate(qh[a], qh[b], (float)p.positions[r] * p.inv_freq[pp], y0, y1);
             }
             qs[n][(a % 8) * NI + a / 8] = y0;
             qs[n][(b % 8) * NI + b / 8] = y1;
@@ -457,12 +469,13 @@ static uint32_t ceil_div32(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 
 
 template <int HD>
 static hipError_t launch_f32_t(const F32Params& fp, uint32_t blocks, const AttnCall& a, hipStream_t s, bool fuse) {
-    if (fuse)
-        hipExtLaunchKernelGGL((attn_f32<HD, true>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0,
-                              fp);
+    if (fuse && fp.rows == 1)
+        hipExtLaunchKernelGGL((attn_f32<HD, 1>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0, fp);
+    else if (fuse)
+        hipExtLaunchKernelGGL((attn_f32<HD, (int)F32_FUSE_ROWS>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before,
+                              a.ev_after, 0, fp);
     else
-        hipExtLaunchKernelGGL((attn_f32<HD, false>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0,
-                              fp);
+        hipExtLaunchKernelGGL((attn_f32<HD, 0>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0, fp);
     return hipGetLastError();
 }
 
@@ -470,7 +483,7 @@ hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipSt
     if (a.rows == 0 || a.nkv == 0 || a.nh % a.nkv != 0 || a.hd == 0 || a.hd % 8 != 0 || a.hd > MAX_HD)
         return hipErrorInvalidValue;
     if (a.tree && a.rows > MAX_ITEMS) return hipErrorInvalidValue;
-    if (rope && (a.tree || a.rows != 1 || kvoff != 0 || rope->rope_dim % 2 || rope->rope_dim > a.hd))
+    if (rope && (a.tree || a.rows > F32_FUSE_ROWS || kvoff != 0 || rope->rope_dim % 2 || rope->rope_dim > a.hd))
         return hipErrorInvalidValue;
     F32Params fp{};
     if (rope) {

@@ -693,6 +693,15 @@ int bchip_rope_append_attention_rows(bchip_ctx* c, float* q, const float* k, con
     CHECK(check_span(c, vc, sat_mul(slots, kvd * esize(kv_type)), "vc"));
     CHECK(check_span(c, positions, (uint64_t)rows * 4, "positions"));
     CHECK(check_span(c, inv_freq, (uint64_t)(rope_dim / 2) * 4, "inv_freq"));
+    if (kv_type == BCHIP_F32 && rows <= 8) {
+        // f32 caches: attn_f32 rotates q and appends the new rows itself (the two calls' bits).
+        const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));
+        AttnCall a{q, kc, vc, kv_type, out, nullptr, 0u, rows, nh, nkv, hd, pos, scale, limit};
+        const RopeArgs r{q, k, v, inv_freq, positions, rope_dim, neox};
+        c->take_marks(a);
+        HIP_TRY(f32_attention(a, 0, c->ws, c->stream, &r), "rope_append_attention_rows");
+        return BCHIP_OK;
+    }
     // (The one-launch form loads the new k and v rows 16 bytes a lane.)
     if (kv_type == BCHIP_F16 && rows > 1 && aligned16(k) && aligned16(v)) {
         const uint64_t limit = std::min(bytes_left(c, kc), bytes_left(c, vc)) / (kvd * esize(kv_type));

@@ -104,9 +104,9 @@ hipError_t shared_attention_fused(const AttnCall& a, const RopeArgs& r, Workspac
 // The left fold of chunk states (attn_combine) over `groups` groups of cp.
 hipError_t combine_launch(CombineParams& cp, uint32_t groups, uint32_t hd, hipStream_t s);
 // Every call on an f32 cache (lines, trees, one row): f32 arithmetic throughout
-// (attention_f32.hip). kvoff: slot offset of the row's cache in a ragged pool. rope (a
-// one-row line call only): the step fused with RoPE and the K/V append of its row at slot
-// a.pos, the bits of rope_append_launch then f32_attention.
+// (attention_f32.hip). kvoff: slot offset of the row's cache in a ragged pool. rope (a line
+// call of at most 8 rows, kvoff 0): the call fused with RoPE and the K/V append of its rows
+// at slots a.pos .., the bits of rope_append_launch then f32_attention.
 hipError_t f32_attention(const AttnCall& a, uint64_t kvoff, Workspace& ws, hipStream_t s,
                          const RopeArgs* rope = nullptr);
 

@@ -171,7 +171,8 @@ int bchip_rope_append_attention(bchip_ctx* ctx, float* q, const float* k, const 
  * rotations, the appends and the attention (its workgroups take the new rows from LDS) for
  * f16 caches at head_dim 128, at most 16 rows with rows x (nh / nkv) <= 64, a line longer
  * than one 192-slot chunk whose split launch fits the device's CUs at once, neox pairs
- * only at rope_dim 64 or 128, and k and v 16-byte aligned; other calls run as the two calls.
+ * only at rope_dim 64 or 128, and k and v 16-byte aligned; and for f32 caches of at most 8
+ * rows at any shape (attn_f32, then its fold when split). Other calls run as the two calls.
  * positions: device u32 [rows]. */
 int bchip_rope_append_attention_rows(bchip_ctx* ctx, float* q, const float* k, const float* v, void* kc, void* vc,
                                      uint32_t kv_type, const float* inv_freq, const uint32_t* positions,

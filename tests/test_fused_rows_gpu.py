@@ -48,6 +48,15 @@ CASES = [
     (8, 32, 8, 64, 64, True, 1e6, bchip.F16, 900),       # head_dim 64: the two calls
     (4, 14, 2, 64, 64, True, 1e6, bchip.F32, 511),       # f32 cache: the two calls
     (1, 32, 8, 128, 128, False, 5e5, bchip.F16, 4096),   # one row: the two calls
+    # f32 caches (attn_f32 rotating q and appending the rows itself, up to 8 rows)
+    (8, 64, 8, 128, 128, False, 5e5, bchip.F32, 4096),   # configs[4]'s verify, split (q by the fold)
+    (8, 32, 8, 128, 128, False, 5e5, bchip.F32, 100),    # one chunk (q by the kernel)
+    (5, 32, 8, 128, 96, True, 1e4, bchip.F32, 190),      # new rows across a chunk boundary, partial neox
+    (8, 16, 16, 64, 64, True, 1e6, bchip.F32, 700),      # 8 rows, one query head a KV head
+    (7, 28, 4, 128, 128, True, 1e6, bchip.F32, 3000),    # four row blocks share the new rows' chunk
+    (9, 28, 4, 128, 128, True, 1e6, bchip.F32, 3000),    # 9 rows: the two calls
+    (3, 14, 2, 64, 64, True, 1e6, bchip.F32, 8000),      # configs[0] heads, a long list (the long fold)
+    (20, 32, 8, 128, 128, False, 5e5, bchip.F32, 700),   # 20 rows: the two calls
 ]
 
 
