@@ -94,6 +94,12 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     __shared__ __attribute__((aligned(16))) float ks[F32_BLK][KS];
     __shared__ __attribute__((aligned(16))) float vs[F32_BLK][HD];
     __shared__ uint32_t tail[MAX_ITEMS];
+    // hd >= 128: each wave's P of a block (two slots at most), read back 16 bytes at a time for
+    // the block sum and P v (eight reads a block where readlane took 32 VALU instructions:
+    // configs[1] over f32 77.7 -> 75.5 us a call, its verify loop 70.8 -> 66.4 us a
+    // layer-step; at hd 64 readlane measured slightly faster).
+    constexpr bool PL = HD >= 128;
+    __shared__ __attribute__((aligned(16))) float pw[PL ? F32_THREADS / 64 : 1][2][PL ? F32_BLK : 4];
     // FUSE: the new K rows (rotated) and V rows as the caches hold them.
     __shared__ __attribute__((aligned(16))) float nrow[FUSE ? 2 : 1][FUSE ? NR : 1][FUSE ? HD : 4];
 
@@ -355,6 +361,11 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
                     pe[s] = exp2_hw(sc - ms);
                 }
                 float bl[NS], acc[NS][DPL];
+                if constexpr (PL) {
+#pragma unroll
+                    for (int s = 0; s < NS; s++)
+                        if (lane < 32u) pw[wave][s][lane] = pe[s];
+                }
 #pragma unroll
                 for (int s = 0; s < NS; s++) {
                     bl[s] = 0.0f;
@@ -363,6 +374,14 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
                 }
 #pragma unroll F32_LU<HD>
                 for (int k8 = 0; k8 < F32_BLK; k8 += 8) {
+                    f32x4 pq[NS][2];
+                    if constexpr (PL) {
+#pragma unroll
+                        for (int s = 0; s < NS; s++) {
+                            pq[s][0] = *(const f32x4*)&pw[wave][s][k8];
+                            pq[s][1] = *(const f32x4*)&pw[wave][s][k8 + 4];
+                        }
+                    }
 #pragma unroll
                     for (int kj = 0; kj < 8; kj++) {
                         const int kk = k8 + kj;
@@ -380,7 +399,8 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
                         }
 #pragma unroll
                         for (int s = 0; s < NS; s++) {
-                            const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe[s]), kk));
+                            const float pk = PL ? pq[s][kj / 4][kj % 4]
+                                                : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe[s]), kk));
                             bl[s] += pk;
 #pragma unroll
                             for (int dd = 0; dd < DPL; dd++) acc[s][dd] += pk * v[dd];
