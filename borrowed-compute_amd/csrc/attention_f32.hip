@@ -72,7 +72,7 @@ constexpr int F32_LU = HD <= 64 ? 2 : 1;
 // workgroups then took two turns of the GPU, 73 -> 96 us a layer-step).
 constexpr uint32_t F32_FUSE_ROWS = 8;
 
-template <int HD, int NR>
+template <int HD, int NR, bool MS>
 __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     constexpr bool FUSE = NR > 0;
     // q and K rows in LDS in lane order: element d = j + 8i at j * NI + i, so that the
@@ -94,12 +94,13 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
     __shared__ __attribute__((aligned(16))) float ks[F32_BLK][KS];
     __shared__ __attribute__((aligned(16))) float vs[F32_BLK][HD];
     __shared__ uint32_t tail[MAX_ITEMS];
-    // hd >= 128: each wave's P of a block (two slots at most), read back 16 bytes at a time for
+    // hd >= 128: each wave's P of a block (its slots of a pass), read back 16 bytes at a time for
     // the block sum and P v (eight reads a block where readlane took 32 VALU instructions:
     // configs[1] over f32 77.7 -> 75.5 us a call, its verify loop 70.8 -> 66.4 us a
     // layer-step; at hd 64 readlane measured slightly faster).
     constexpr bool PL = HD >= 128;
-    __shared__ __attribute__((aligned(16))) float pw[PL ? F32_THREADS / 64 : 1][2][PL ? F32_BLK : 4];
+    constexpr int PS = MS ? F32_SLOTS / (F32_THREADS / 64) : 1;  // slots of a pass at most (one without MS)
+    __shared__ __attribute__((aligned(16))) float pw[PL ? F32_THREADS / 64 : 1][PL ? PS : 1][PL ? F32_BLK : 4];
     // FUSE: the new K rows (rotated) and V rows as the caches hold them.
     __shared__ __attribute__((aligned(16))) float nrow[FUSE ? 2 : 1][FUSE ? NR : 1][FUSE ? HD : 4];
 
@@ -314,6 +315,7 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             // in the same order; K's and V's LDS reads serve all of them.
             auto pass = [&](auto S0, auto NSc) {
                 constexpr int s0 = decltype(S0)::value, NS = decltype(NSc)::value;
+                static_assert(s0 + NS <= SPW && (!PL || NS <= PS), "a pass's slots are the wave's, its P rows in pw");
                 uint32_t nn[NS];
                 float a[NS][4];
 #pragma unroll
@@ -422,7 +424,19 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
             static_assert(SPW == 4, "four slots a wave at most");
             // The wave's slots that may hold a query: wave, wave + W, ... below nused.
             const uint32_t nact = wave < nused ? min((uint32_t)SPW, (nused - wave + W - 1) / W) : 0u;
-            if constexpr (HD <= 64) {
+            if constexpr (MS && HD > 64) {
+                // A launch whose waves hold several slots (MS: more than four in a workgroup):
+                // four a pass where a wave has four, else two.
+                if (nact == 4) {
+                    pass(i0{}, std::integral_constant<int, 4>{});
+                } else {
+                    if (nact >= 2)
+                        pass(i0{}, i2{});
+                    else if (nact == 1)
+                        pass(i0{}, i1{});
+                    if (nact == 3) pass(i2{}, i1{});
+                }
+            } else if constexpr (HD <= 64) {
                 // Two slots a pass: the shared reads and the two slots' chains side by side
                 // (configs[0], seven slots over four waves: 22.7 -> 21.9 us a layer-step).
                 if (nact >= 2)
@@ -487,15 +501,30 @@ __global__ __launch_bounds__(F32_THREADS) void attn_f32(const F32Params p) {
 
 static uint32_t ceil_div32(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
+template <int HD, bool MS>
+static void launch_f32_ms(const F32Params& fp, uint32_t blocks, const AttnCall& a, hipStream_t s, bool fuse) {
+    if (fuse && fp.rows == 1)
+        hipExtLaunchKernelGGL((attn_f32<HD, 1, MS>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0,
+                              fp);
+    else if (fuse)
+        hipExtLaunchKernelGGL((attn_f32<HD, (int)F32_FUSE_ROWS, MS>), dim3(blocks), dim3(F32_THREADS), 0, s,
+                              a.ev_before, a.ev_after, 0, fp);
+    else
+        hipExtLaunchKernelGGL((attn_f32<HD, 0, MS>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0,
+                              fp);
+}
+
+// MS: a launch whose workgroups hold more than four query slots (a wave then has several);
+// its own kernels, so that the one-slot-a-wave step keeps the registers of one pass.
 template <int HD>
 static hipError_t launch_f32_t(const F32Params& fp, uint32_t blocks, const AttnCall& a, hipStream_t s, bool fuse) {
-    if (fuse && fp.rows == 1)
-        hipExtLaunchKernelGGL((attn_f32<HD, 1>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0, fp);
-    else if (fuse)
-        hipExtLaunchKernelGGL((attn_f32<HD, (int)F32_FUSE_ROWS>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before,
-                              a.ev_after, 0, fp);
-    else
-        hipExtLaunchKernelGGL((attn_f32<HD, 0>), dim3(blocks), dim3(F32_THREADS), 0, s, a.ev_before, a.ev_after, 0, fp);
+    if constexpr (HD > 64) {
+        if (fp.G * fp.rb > (uint32_t)(F32_THREADS / 64)) {
+            launch_f32_ms<HD, true>(fp, blocks, a, s, fuse);
+            return hipGetLastError();
+        }
+    }
+    launch_f32_ms<HD, false>(fp, blocks, a, s, fuse);
     return hipGetLastError();
 }
 
