@@ -125,3 +125,27 @@ def test_ragged_decode_step_f32_and_unfused_shapes(ctx):
     """f32 pools, and shapes the fused kernel does not take, run as the two calls."""
     ragged_step(ctx, [7, 300, 5, 129], bchip.F32, 14, 2, 64, 64, True, 1e6, 60)
     ragged_step(ctx, [7, 300, 5, 129], bchip.F16, 16, 1, 128, 128, False, 5e5, 70)
+
+
+def _ragged_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        nseq = int(rng.integers(1, 25))
+        lens = [int(x) for x in rng.integers(1, 6000, nseq)]
+        hd = int(rng.choice([64, 128, 128, 256]))
+        nkv = int(rng.choice([1, 2, 4, 8]))
+        g = int(rng.choice([1, 2, 4, 7, 8]))
+        rd = int(rng.choice([hd, hd // 2]))
+        neox = bool(rng.random() < 0.5)
+        kv_type = bchip.F16 if rng.random() < 0.75 else bchip.F32
+        cases.append((lens, kv_type, g * nkv, nkv, hd, rd, neox, int(rng.integers(1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("lens,kv_type,nh,nkv,hd,rd,neox,seed", _ragged_cases(12, 4242))
+def test_ragged_decode_step_seeded_sweep(ctx, lens, kv_type, nh, nkv, hd, rd, neox, seed):
+    """Random pools (1-24 sequences of 1-6000 slots), heads, head dims and rotary shapes: the
+    one launch against the two calls and each sequence's own step bit for bit, and every
+    sequence against the oracle."""
+    ragged_step(ctx, lens, kv_type, nh, nkv, hd, rd, neox, 1e4, seed % 100000)
