@@ -42,7 +42,13 @@ def _attention_cases(n, seed):
     return cases
 
 
-@pytest.mark.parametrize("rows,pos,nh,nkv,hd,tree,kv_type,seed", _attention_cases(120, 20261202))
+# Long lists beside the sweep: a verify pass past the group fold's reach (more than 32 chunks:
+# the long fold), the same over f32, a tree at 9000 slots, a line of 100 rows at 12000.
+LONG = [(8, 35000, 64, 8, 128, False, bchip.F16, 1), (8, 35000, 64, 8, 128, False, bchip.F32, 2),
+        (40, 9000, 32, 8, 128, True, bchip.F16, 3), (100, 12000, 8, 2, 128, False, bchip.F16, 4)]
+
+
+@pytest.mark.parametrize("rows,pos,nh,nkv,hd,tree,kv_type,seed", LONG + _attention_cases(120, 20261202))
 def test_attention_against_the_oracle(ctx, rows, pos, nh, nkv, hd, tree, kv_type, seed):
     rng = np.random.default_rng(seed)
     kvd = nkv * hd
