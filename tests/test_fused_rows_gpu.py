@@ -42,6 +42,8 @@ CASES = [
     (8, 32, 8, 128, 96, False, 1e4, bchip.F16, 800),     # partial rotary, adjacent pairs (fused)
     (8, 32, 8, 128, 96, True, 1e4, bchip.F16, 800),      # neox pairs 48 dims apart: the two calls
     (16, 64, 16, 128, 128, False, 5e5, bchip.F16, 500),  # 16 rows, 4 query heads a KV head (fused)
+    (4, 16, 1, 128, 128, False, 5e5, bchip.F16, 3000),   # 16 query heads a KV head, 4 rows (fused)
+    (16, 32, 8, 128, 64, True, 1e4, bchip.F16, 2500),    # 16 rows, neox over half the dims (fused)
     (8, 64, 8, 128, 128, False, 5e5, bchip.F16, 100),    # one chunk: the two calls
     (20, 32, 8, 128, 128, False, 5e5, bchip.F16, 700),   # 80 slots a KV head: the two calls
     (8, 16, 16, 128, 128, False, 5e5, bchip.F16, 900),   # one query head a KV head (fused)
