@@ -566,12 +566,13 @@ __global__ __launch_bounds__(256, sizeof(KVT) == 2 && HD <= 128 ? 4 : 2) void at
 // folded left to right from a cleared state, then attn_row_fold's order over the runs. A
 // launch of many units (RUNS: a ragged batch, whose lists keep the chunks they would have
 // alone) gives each wave a whole run: it folds the run's chunks itself, in that order, and
-// writes one state a run (a quarter of the states written and read back); the bits are
-// those of a unit a chunk.
+// writes one state a run (an eighth of the states written and read back); the bits are
+// those of a unit a chunk. Runs of eight against four: configs[3]'s ragged call 127.2 ->
+// 125.3 us (medians of four interleaved runs), the 32768-slot step unchanged (28.5-28.7).
 constexpr int RB = 32;                     // list entries per block of the one-row kernel
 constexpr uint32_t ROW_FUSE_MAXG = 8;      // query heads per KV head a fused step takes
 constexpr uint32_t ROW_MAX_CHUNKS = 256;   // chunks per (item, KV head): attn_row_fold's reach
-constexpr uint32_t ROW_RUN = 4;            // chunks a run
+constexpr uint32_t ROW_RUN = 8;            // chunks a run
 
 template <int HD, typename KVT, bool FUSE, bool RUNS>
 __global__ __launch_bounds__(256, 2) void attn_decode_row(const DirectParams p) {
@@ -2973,9 +2974,9 @@ static hipError_t row_launch(const AttnCall& a, const Item* items, uint32_t nite
         units += (uint64_t)a.nkv * I.nchunk;
         fold = fold || I.nchunk > 1;
     }
-    // A unit a chunk, or a unit a run of ROW_RUN chunks where that still leaves ROW_UNITS
+    // A unit a chunk, or a unit a run of ROW_RUN chunks for a launch of 4 ROW_UNITS chunk
     // units or more (a ragged batch of long lists).
-    dp.runs = ws.row_runs == 2 || (ws.row_runs == 1 && units >= ROW_RUN * ROW_UNITS);
+    dp.runs = ws.row_runs == 2 || (ws.row_runs == 1 && units >= 4 * ROW_UNITS);
     // The items of the longest chunks first, so that the launch's last workgroups are its
     // shortest (an item's place in the launch changes none of its arithmetic).
     std::stable_sort(dp.items, dp.items + nitems, [](const Item& x, const Item& y) { return x.chunk > y.chunk; });

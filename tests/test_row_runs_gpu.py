@@ -1,8 +1,7 @@
 """One-row launches with a unit a run of chunks against a unit a chunk (BCHIP_ROW_RUNS=2 and
-=0 at init; the default takes runs from ROW_RUN * ROW_UNITS chunk units, a ragged batch of
-long lists).
+=0 at init; the default takes runs from 4096 chunk units, a ragged batch of long lists).
 
-The fold of a one-row list's chunk states is fixed by the list alone: runs of four
+The fold of a one-row list's chunk states is fixed by the list alone: runs of eight
 consecutive chunks, each folded left to right from a cleared state, then attn_row_fold's
 order over the runs. With runs, the decode wave that streams a run folds its chunks itself
 and writes one state; without, attn_row_fold folds the run from the chunk states. Outputs,
