@@ -49,7 +49,7 @@ struct F32Params {
     uint32_t split;   // a workgroup per chunk
     const float* zero;  // ZERO_BYTES of zeros: the loads of rows past a list
     // A line call fused with RoPE and the K/V append of its rows at slots pos .. pos + rows - 1
-    // (attn_f32<HD, NR>, NR > 0: at most NR rows): q is unrotated on entry and rotated as it
+    // (attn_f32<HD, NR, MS>, NR > 0: at most NR rows): q is unrotated on entry and rotated as it
     // is staged; the new K rows (knew, rotated here) and V rows (vnew) go to the caches and
     // stand in for those slots' cache entries. q is left rotated: by the workgroup itself when
     // unsplit, else by the fold.
