@@ -652,9 +652,20 @@ def main():
         log(json.dumps(cpu))
         extra["cpu_per_config"] = cpu_per_config()
         log(json.dumps(extra["cpu_per_config"]))
+    # The rate a plain copy reaches in the same run (bytes read + written over its time):
+    # the measured ceiling the kernel and the call are also reported against.
+    ceil_gbs = (extra.get("copy_calibration") or {}).get("copy_GBps")
+    if ceil_gbs and "ragged_qwen7b" in extra:
+        rg = extra["ragged_qwen7b"]
+        rg["frac_of_copy"], rg["call_frac_of_copy"] = rg["GBps"] / ceil_gbs, rg["call_GBps"] / ceil_gbs
     if head is None:
         print(json.dumps({"extra": extra, "cpu_baseline": cpu}))
         return
+    measured = None
+    if ceil_gbs:
+        measured = {"what": "a plain 256 MiB f16 copy (bchip_copy) in the same run, read + write bytes over its time",
+                    "GBps": ceil_gbs, "kernel_frac": head["attn_GBps"] / ceil_gbs,
+                    "call_frac": head["call_GBps"] / ceil_gbs}
     line = {
         "metric": METRIC,
         "value": head["tokens_per_s"],
@@ -678,7 +689,8 @@ def main():
                      "kernel": "attn_decode_row<128, f16, fused> (bchip_rope_append_attention's attention kernel)",
                      "bytes_per_launch": head["attn_bytes_per_launch"], "launch_us": head["attn_kernel_us"],
                      "call": {"what": "the whole per-layer call: decode kernel, chunk fold, launch gaps",
-                              "us": head["call_us"], "GBps": head["call_GBps"], "frac": head["call_hbm_frac"]}},
+                              "us": head["call_us"], "GBps": head["call_GBps"], "frac": head["call_hbm_frac"]},
+                     "measured_ceiling": measured},
         "cpu_baseline": cpu,
         "extra": extra,
     }
